@@ -1,0 +1,604 @@
+// Causal multi-head attention on gfx950 fp32 matrix cores, d_head ∈ {8,16,32,64}.
+//
+// Reference semantics (src/attention.rs:396-550, src/gpu/attention.rs:21-331):
+//   S = Q_h K_hᵀ / sqrt(d_head), S[i,j] = -inf for j > i, P = softmax_rows(S),
+//   O_h = P V_h;  backward: dP = dO Vᵀ, rowdot_i = Σ_j P_ij dP_ij,
+//   dS = P ⊙ (dP − rowdot), dQ += scale·dS K, dK += scale·dSᵀ Q, dV += Pᵀ dO.
+//
+// Instead of materialising P ([H,T,T] in the reference) the forward keeps
+// the running row max / row sum of a flash-style tile loop and stores one
+// log-sum-exp per row; the backward recomputes P tile by tile from it.
+// rowdot_i equals Σ_c dO_ic O_ic, computed once per row (pass 1).  dQ is
+// produced by a pass over key tiles (pass 2) and dK/dV by a pass over query
+// tiles (pass 3), so every output element has exactly one writer: the
+// backward is deterministic, like the reference's 3-dispatch scheme.
+//
+// MFMA layout (v_mfma_f32_16x16x4_f32, see common.hpp).  A wave owns 16 rows
+// (queries in the forward and dQ pass, keys in the dK/dV pass).  Scores are
+// computed transposed (Sᵀ = K·Qᵀ), which leaves lane l holding column l%16
+// of Sᵀ — all of them scores of ONE query row — so the softmax statistics
+// are per-lane scalars and the Sᵀ accumulator registers are directly the
+// B operand of the next product (Oᵀ = Vᵀ·Pᵀ).  The row max is reduced over
+// the four 16-lane groups with cross-lane swizzles (shfl_xor 16, 32).
+// The head dimension is covered in chunks of 16 (NC = ceil(DH/16)); for
+// DH = 8 the upper half of the single chunk is zero.
+#include "common.hpp"
+
+namespace {
+
+constexpr int TQ = 64;  // rows per tile (4 waves × 16)
+constexpr float LOG2E = 1.4426950408889634f;
+
+struct AttnArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* o;    // forward output (bwd pass 1)
+  const float* dO;   // gradient of the output
+  float* out;        // forward output
+  float* lse;        // [B, H, T]
+  float* D;          // [B, H, T] rowdot
+  float* dq;
+  float* dk;
+  float* dv;
+  int ld_qkv;        // row stride of q, k, v
+  int ld_o;          // row stride of out / o / dO
+  int ld_d;          // row stride of dq, dk, dv
+  int T, H;
+  float scale;       // 1/sqrt(d_head)
+};
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+template <int DH>
+struct Geo {
+  static constexpr int NC = (DH + 15) / 16;  // 16-wide chunks of the head dim
+  static constexpr int LDT = NC * 16 + 4;    // padded LDS row stride (floats)
+  static constexpr int TILE = TQ * LDT;
+  static constexpr int F4 = TQ * DH / 4;     // float4 per [64 × DH] tile
+  static constexpr int NV = (F4 + 255) / 256;
+  // Does a float4 at head-dim offset `d` hold real data?
+  __device__ static __forceinline__ bool live(int d) { return DH % 16 == 0 || d < DH; }
+};
+
+// A [64 rows × DH] fp32 tile (rows r0.., zero-filled at r >= T) copied from a
+// row-major source with row stride ld into registers, then into LDS.  LDS
+// columns past DH (DH = 8) are zero-filled once by zero_pad_cols.
+template <int DH>
+struct TileRegs {
+  using G = Geo<DH>;
+  floatx4 v[G::NV];
+  __device__ __forceinline__ void load(const float* __restrict__ base, int ld, int r0, int T,
+                                       int tid) {
+#pragma unroll
+    for (int i = 0; i < G::NV; ++i) {
+      const int f = tid + i * 256;
+      const int r = f / (DH / 4), c = (f % (DH / 4)) * 4;
+      floatx4 x = {0.f, 0.f, 0.f, 0.f};
+      if (f < G::F4 && r0 + r < T) x = *reinterpret_cast<const floatx4*>(base + (size_t)(r0 + r) * ld + c);
+      v[i] = x;
+    }
+  }
+  __device__ __forceinline__ void store(float* __restrict__ s, int tid) const {
+#pragma unroll
+    for (int i = 0; i < G::NV; ++i) {
+      const int f = tid + i * 256;
+      const int r = f / (DH / 4), c = (f % (DH / 4)) * 4;
+      if (f < G::F4) *reinterpret_cast<floatx4*>(s + r * G::LDT + c) = v[i];
+    }
+  }
+};
+
+template <int DH>
+__device__ __forceinline__ void zero_pad_cols(float* s, int tid) {
+  using G = Geo<DH>;
+  if (DH % 16 != 0) {
+    for (int i = tid; i < TQ * (G::NC * 16 - DH); i += 256) {
+      const int r = i / (G::NC * 16 - DH), c = DH + i % (G::NC * 16 - DH);
+      s[r * G::LDT + c] = 0.f;
+    }
+  }
+}
+
+// This lane's operand values of a 16-row slab:
+// f[c][s] = X[row][16c + 4·(lane/16) + s]  (zero past DH or at row >= T).
+template <int DH>
+__device__ __forceinline__ void load_rows_frag(floatx4* f, const float* __restrict__ base, int ld,
+                                               int row, int T, int g) {
+#pragma unroll
+  for (int c = 0; c < Geo<DH>::NC; ++c) {
+    floatx4 x = {0.f, 0.f, 0.f, 0.f};
+    if (row < T && Geo<DH>::live(16 * c + 4 * g))
+      x = *reinterpret_cast<const floatx4*>(base + (size_t)row * ld + 16 * c + 4 * g);
+    f[c] = x;
+  }
+}
+
+// ---------------------------------------------------------------- forward
+template <int DH>
+__global__ void __launch_bounds__(256) mha_fwd_kernel(AttnArgs a) {
+  using G = Geo<DH>;
+  constexpr int NC = G::NC, LDT = G::LDT;
+  __shared__ __attribute__((aligned(16))) float sm[2][2][G::TILE];  // [stage][K,V]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int nqt = (a.T + TQ - 1) / TQ;
+  const int qt = nqt - 1 - blockIdx.x;  // heaviest (longest) query tiles first
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int q0 = qt * TQ;
+  const size_t row_base = (size_t)b * a.T;
+  const float* Qb = a.q + row_base * a.ld_qkv + h * DH;
+  const float* Kb = a.k + row_base * a.ld_qkv + h * DH;
+  const float* Vb = a.v + row_base * a.ld_qkv + h * DH;
+
+  const int qrow = q0 + 16 * w + l16;  // this lane's query row (Sᵀ column)
+  floatx4 qf[NC];
+  load_rows_frag<DH>(qf, Qb, a.ld_qkv, qrow, a.T, g);
+
+  const float sl2 = a.scale * LOG2E;  // scores kept in the log2 domain
+  float m = -INFINITY, l = 0.f;
+  floatx4 acc_o[NC];
+#pragma unroll
+  for (int d = 0; d < NC; ++d) acc_o[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  zero_pad_cols<DH>(sm[0][0], tid);
+  zero_pad_cols<DH>(sm[0][1], tid);
+  zero_pad_cols<DH>(sm[1][0], tid);
+  zero_pad_cols<DH>(sm[1][1], tid);
+  TileRegs<DH> rk, rv;
+  rk.load(Kb, a.ld_qkv, 0, a.T, tid);
+  rv.load(Vb, a.ld_qkv, 0, a.T, tid);
+  rk.store(sm[0][0], tid);
+  rv.store(sm[0][1], tid);
+  __syncthreads();
+
+  for (int kt = 0; kt <= qt; ++kt) {
+    const int cur = kt & 1;
+    if (kt < qt) {
+      rk.load(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
+      rv.load(Vb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
+    }
+    const float* Ks = sm[cur][0];
+    const float* Vs = sm[cur][1];
+    const int k0 = kt * TQ;
+    // Key sub-tiles j > w of the diagonal tile are entirely in the future.
+    const int jmax = (kt == qt) ? w : 3;
+
+    floatx4 st[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      st[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+      if (j <= jmax) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const floatx4 kf = *reinterpret_cast<const floatx4*>(Ks + (16 * j + l16) * LDT + 16 * c + 4 * g);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) st[j] = mfma16x16x4(kf[s], qf[c][s], st[j]);
+        }
+      }
+    }
+    // Scale, mask, tile row max.  st[j][e] = S[qrow][k0 + 16j + 4g + e].
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = k0 + 16 * j + 4 * g + e;
+        float s = st[j][e] * sl2;
+        if (j > jmax || key > qrow || key >= a.T) s = -INFINITY;
+        st[j][e] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = fmaxf(mx, shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = exp2f(m - m_new);
+    m = m_new;
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = exp2f(st[j][e] - m_new);
+        st[j][e] = p;
+        ps += p;
+      }
+    l = l * alpha + ps;
+#pragma unroll
+    for (int d = 0; d < NC; ++d) acc_o[d] *= alpha;
+    // Oᵀ[d][q] += Vᵀ[d][key] · Pᵀ[key][q]
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j <= jmax) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const float* vr = Vs + (16 * j + 4 * g + s) * LDT + l16;
+#pragma unroll
+          for (int d = 0; d < NC; ++d) acc_o[d] = mfma16x16x4(vr[16 * d], st[j][s], acc_o[d]);
+        }
+      }
+    }
+    if (kt < qt) {
+      rk.store(sm[cur ^ 1][0], tid);
+      rv.store(sm[cur ^ 1][1], tid);
+    }
+    __syncthreads();
+  }
+
+  l += shfl_xor(l, 16);
+  l += shfl_xor(l, 32);
+  if (qrow < a.T) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    float* orow = a.out + (row_base + qrow) * a.ld_o + h * DH;
+#pragma unroll
+    for (int d = 0; d < NC; ++d)
+      if (G::live(16 * d + 4 * g))
+        *reinterpret_cast<floatx4*>(orow + 16 * d + 4 * g) = acc_o[d] * inv;
+    if (g == 0) a.lse[((size_t)b * a.H + h) * a.T + qrow] = (m + __log2f(l)) * (1.f / LOG2E);
+  }
+}
+
+// ------------------------------------------------- backward pass 1: rowdot
+// D[b,h,i] = Σ_c dO[i,c]·O[i,c]  (= Σ_j P_ij dP_ij of the reference's fused
+// dscores pass, src/gpu/attention.rs:163-247).  DH/4 lanes per (row, head).
+template <int DH>
+__global__ void __launch_bounds__(256) mha_bwd_rowdot_kernel(AttnArgs a, int B) {
+  constexpr int LPR = DH / 4;            // lanes per row
+  constexpr int RPB = 256 / LPR;         // rows per block
+  const int gid = blockIdx.x * RPB + threadIdx.x / LPR;  // (b, t, h) flattened
+  const int part = threadIdx.x % LPR;
+  const int total = B * a.T * a.H;
+  float s = 0.f;
+  int h = 0, bt = 0;
+  if (gid < total) {
+    h = gid % a.H;
+    bt = gid / a.H;
+    const floatx4 o = *reinterpret_cast<const floatx4*>(a.o + (size_t)bt * a.ld_o + h * DH + 4 * part);
+    const floatx4 d = *reinterpret_cast<const floatx4*>(a.dO + (size_t)bt * a.ld_o + h * DH + 4 * part);
+    s = o[0] * d[0] + o[1] * d[1] + o[2] * d[2] + o[3] * d[3];
+  }
+#pragma unroll
+  for (int m = LPR / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
+  if (gid < total && part == 0) {
+    const int b = bt / a.T, t = bt % a.T;
+    a.D[((size_t)b * a.H + h) * a.T + t] = s;
+  }
+}
+
+// ---------------------------------------------------- backward pass 2: dQ
+template <int DH>
+__global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
+  using G = Geo<DH>;
+  constexpr int NC = G::NC, LDT = G::LDT;
+  __shared__ __attribute__((aligned(16))) float sm[2][2][G::TILE];  // [stage][K,V]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int nqt = (a.T + TQ - 1) / TQ;
+  const int qt = nqt - 1 - blockIdx.x;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int q0 = qt * TQ;
+  const size_t row_base = (size_t)b * a.T;
+  const float* Qb = a.q + row_base * a.ld_qkv + h * DH;
+  const float* Kb = a.k + row_base * a.ld_qkv + h * DH;
+  const float* Vb = a.v + row_base * a.ld_qkv + h * DH;
+  const float* dOb = a.dO + row_base * a.ld_o + h * DH;
+
+  const int qrow = q0 + 16 * w + l16;
+  floatx4 qf[NC], df[NC];
+  load_rows_frag<DH>(qf, Qb, a.ld_qkv, qrow, a.T, g);
+  load_rows_frag<DH>(df, dOb, a.ld_o, qrow, a.T, g);
+  const size_t stat = ((size_t)b * a.H + h) * a.T;
+  const float lse2 = qrow < a.T ? a.lse[stat + qrow] * LOG2E : 0.f;
+  const float Dq = qrow < a.T ? a.D[stat + qrow] : 0.f;
+  const float sl2 = a.scale * LOG2E;
+
+  floatx4 acc[NC];
+#pragma unroll
+  for (int d = 0; d < NC; ++d) acc[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  zero_pad_cols<DH>(sm[0][0], tid);
+  zero_pad_cols<DH>(sm[0][1], tid);
+  zero_pad_cols<DH>(sm[1][0], tid);
+  zero_pad_cols<DH>(sm[1][1], tid);
+  TileRegs<DH> rk, rv;
+  rk.load(Kb, a.ld_qkv, 0, a.T, tid);
+  rv.load(Vb, a.ld_qkv, 0, a.T, tid);
+  rk.store(sm[0][0], tid);
+  rv.store(sm[0][1], tid);
+  __syncthreads();
+
+  for (int kt = 0; kt <= qt; ++kt) {
+    const int cur = kt & 1;
+    if (kt < qt) {
+      rk.load(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
+      rv.load(Vb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
+    }
+    const float* Ks = sm[cur][0];
+    const float* Vs = sm[cur][1];
+    const int k0 = kt * TQ;
+    const int jmax = (kt == qt) ? w : 3;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j > jmax) continue;
+      floatx4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const floatx4 kf = *reinterpret_cast<const floatx4*>(Ks + (16 * j + l16) * LDT + 16 * c + 4 * g);
+        const floatx4 vf = *reinterpret_cast<const floatx4*>(Vs + (16 * j + l16) * LDT + 16 * c + 4 * g);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          st = mfma16x16x4(kf[s], qf[c][s], st);  // Sᵀ[key][q]
+          dp = mfma16x16x4(vf[s], df[c][s], dp);  // dPᵀ[key][q]
+        }
+      }
+      // dSᵀ = Pᵀ ⊙ (dPᵀ − D_q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = k0 + 16 * j + 4 * g + e;
+        float p = exp2f(st[e] * sl2 - lse2);
+        if (key > qrow || key >= a.T) p = 0.f;
+        st[e] = p * (dp[e] - Dq);
+      }
+      // dQᵀ[d][q] += Kᵀ[d][key] · dSᵀ[key][q]
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float* kr = Ks + (16 * j + 4 * g + s) * LDT + l16;
+#pragma unroll
+        for (int d = 0; d < NC; ++d) acc[d] = mfma16x16x4(kr[16 * d], st[s], acc[d]);
+      }
+    }
+    if (kt < qt) {
+      rk.store(sm[cur ^ 1][0], tid);
+      rv.store(sm[cur ^ 1][1], tid);
+    }
+    __syncthreads();
+  }
+  if (qrow < a.T) {
+    float* dqr = a.dq + (row_base + qrow) * a.ld_d + h * DH;
+#pragma unroll
+    for (int d = 0; d < NC; ++d) {
+      if (!G::live(16 * d + 4 * g)) continue;
+      floatx4* p = reinterpret_cast<floatx4*>(dqr + 16 * d + 4 * g);
+      *p = *p + acc[d] * a.scale;
+    }
+  }
+}
+
+// ------------------------------------------------- backward pass 3: dK, dV
+template <int DH>
+__global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
+  using G = Geo<DH>;
+  constexpr int NC = G::NC, LDT = G::LDT;
+  __shared__ __attribute__((aligned(16))) float sm[2][2][G::TILE];  // [stage][Q,dO]
+  __shared__ __attribute__((aligned(16))) float st_lse[2][TQ];
+  __shared__ __attribute__((aligned(16))) float st_D[2][TQ];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int nqt = (a.T + TQ - 1) / TQ;
+  const int kt = blockIdx.x;  // key tile 0 has the most work: launched first
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int k0 = kt * TQ;
+  const size_t row_base = (size_t)b * a.T;
+  const float* Qb = a.q + row_base * a.ld_qkv + h * DH;
+  const float* Kb = a.k + row_base * a.ld_qkv + h * DH;
+  const float* Vb = a.v + row_base * a.ld_qkv + h * DH;
+  const float* dOb = a.dO + row_base * a.ld_o + h * DH;
+  const size_t stat = ((size_t)b * a.H + h) * a.T;
+
+  const int krow = k0 + 16 * w + l16;  // this lane's key (column of S)
+  floatx4 kf[NC], vf[NC];
+  load_rows_frag<DH>(kf, Kb, a.ld_qkv, krow, a.T, g);
+  load_rows_frag<DH>(vf, Vb, a.ld_qkv, krow, a.T, g);
+  const float sl2 = a.scale * LOG2E;
+
+  floatx4 acc_k[NC], acc_v[NC];
+#pragma unroll
+  for (int d = 0; d < NC; ++d) {
+    acc_k[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+    acc_v[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  zero_pad_cols<DH>(sm[0][0], tid);
+  zero_pad_cols<DH>(sm[0][1], tid);
+  zero_pad_cols<DH>(sm[1][0], tid);
+  zero_pad_cols<DH>(sm[1][1], tid);
+  TileRegs<DH> rq, rd;
+  float r_lse = 0.f, r_D = 0.f;
+  auto load_stats = [&](int q0) {
+    if (tid < TQ) {
+      const int q = q0 + tid;
+      r_lse = q < a.T ? a.lse[stat + q] * LOG2E : 0.f;
+      r_D = q < a.T ? a.D[stat + q] : 0.f;
+    }
+  };
+  rq.load(Qb, a.ld_qkv, k0, a.T, tid);
+  rd.load(dOb, a.ld_o, k0, a.T, tid);
+  load_stats(k0);
+  rq.store(sm[0][0], tid);
+  rd.store(sm[0][1], tid);
+  if (tid < TQ) {
+    st_lse[0][tid] = r_lse;
+    st_D[0][tid] = r_D;
+  }
+  __syncthreads();
+
+  for (int qt = kt; qt < nqt; ++qt) {
+    const int cur = (qt - kt) & 1;
+    const bool more = qt + 1 < nqt;
+    if (more) {
+      rq.load(Qb, a.ld_qkv, (qt + 1) * TQ, a.T, tid);
+      rd.load(dOb, a.ld_o, (qt + 1) * TQ, a.T, tid);
+      load_stats((qt + 1) * TQ);
+    }
+    const float* Qs = sm[cur][0];
+    const float* dOs = sm[cur][1];
+    const int q0 = qt * TQ;
+    // Query sub-tiles jq < w of the diagonal tile lie entirely before this
+    // wave's keys: fully masked.
+    const int jmin = (qt == kt) ? w : 0;
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      if (jq < jmin) continue;
+      floatx4 s_ = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const floatx4 qv = *reinterpret_cast<const floatx4*>(Qs + (16 * jq + l16) * LDT + 16 * c + 4 * g);
+        const floatx4 dv_ = *reinterpret_cast<const floatx4*>(dOs + (16 * jq + l16) * LDT + 16 * c + 4 * g);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          s_ = mfma16x16x4(qv[s], kf[c][s], s_);   // S[q][key]
+          dp = mfma16x16x4(dv_[s], vf[c][s], dp);  // dP[q][key]
+        }
+      }
+      const floatx4 lq = *reinterpret_cast<const floatx4*>(&st_lse[cur][16 * jq + 4 * g]);
+      const floatx4 Dq = *reinterpret_cast<const floatx4*>(&st_D[cur][16 * jq + 4 * g]);
+      floatx4 p, ds;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int q = q0 + 16 * jq + 4 * g + e;
+        float pe = exp2f(s_[e] * sl2 - lq[e]);
+        if (krow > q || q >= a.T) pe = 0.f;
+        p[e] = pe;
+        ds[e] = pe * (dp[e] - Dq[e]);
+      }
+      // dVᵀ[d][key] += dOᵀ[d][q]·P[q][key];  dKᵀ[d][key] += Qᵀ[d][q]·dS[q][key]
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float* dor = dOs + (16 * jq + 4 * g + s) * LDT + l16;
+        const float* qr = Qs + (16 * jq + 4 * g + s) * LDT + l16;
+#pragma unroll
+        for (int d = 0; d < NC; ++d) {
+          acc_v[d] = mfma16x16x4(dor[16 * d], p[s], acc_v[d]);
+          acc_k[d] = mfma16x16x4(qr[16 * d], ds[s], acc_k[d]);
+        }
+      }
+    }
+    if (more) {
+      rq.store(sm[cur ^ 1][0], tid);
+      rd.store(sm[cur ^ 1][1], tid);
+      if (tid < TQ) {
+        st_lse[cur ^ 1][tid] = r_lse;
+        st_D[cur ^ 1][tid] = r_D;
+      }
+    }
+    __syncthreads();
+  }
+  if (krow < a.T) {
+    float* dkr = a.dk + (row_base + krow) * a.ld_d + h * DH;
+    float* dvr = a.dv + (row_base + krow) * a.ld_d + h * DH;
+#pragma unroll
+    for (int d = 0; d < NC; ++d) {
+      if (!G::live(16 * d + 4 * g)) continue;
+      floatx4* pk = reinterpret_cast<floatx4*>(dkr + 16 * d + 4 * g);
+      floatx4* pv = reinterpret_cast<floatx4*>(dvr + 16 * d + 4 * g);
+      *pk = *pk + acc_k[d] * a.scale;
+      *pv = *pv + acc_v[d];
+    }
+  }
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+bool dh_supported(uint32_t d) { return d == 8 || d == 16 || d == 32 || d == 64; }
+
+int check_common(aur_ctx* ctx, uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head,
+                 uint32_t ld_qkv, uint32_t ld_o) {
+  if (!dh_supported(d_head))
+    return aur::set_error(ctx, AUR_ELIMIT, "attention: d_head=%u, kernels support 8/16/32/64", d_head);
+  if (b == 0 || t == 0 || n_head == 0) return aur::set_error(ctx, AUR_EINVAL, "attention: empty shape");
+  if (ld_qkv < n_head * d_head || ld_o < n_head * d_head || (ld_qkv & 3) || (ld_o & 3))
+    return aur::set_error(ctx, AUR_EINVAL, "attention: bad row stride (%u, %u)", ld_qkv, ld_o);
+  if (n_head > 65535 || b > 65535) return aur::set_error(ctx, AUR_ELIMIT, "attention: grid too large");
+  return 0;
+}
+
+template <int DH>
+void launch_fwd(const AttnArgs& a, int b, hipStream_t st) {
+  dim3 grid((a.T + TQ - 1) / TQ, a.H, b);
+  hipLaunchKernelGGL(mha_fwd_kernel<DH>, grid, dim3(256), 0, st, a);
+}
+
+template <int DH>
+void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
+  constexpr int RPB = 256 / (DH / 4);
+  const size_t rows = (size_t)b * a.T * a.H;
+  hipLaunchKernelGGL(mha_bwd_rowdot_kernel<DH>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256),
+                     0, st, a, b);
+  dim3 grid((a.T + TQ - 1) / TQ, a.H, b);
+  hipLaunchKernelGGL(mha_bwd_dq_kernel<DH>, grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL(mha_bwd_dkv_kernel<DH>, grid, dim3(256), 0, st, a);
+}
+
+}  // namespace
+
+extern "C" {
+
+int aur_mha_fwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v, uint32_t ld_qkv,
+                   float* out, uint32_t ld_out, float* lse, uint32_t b, uint32_t t,
+                   uint32_t n_head, uint32_t d_head) {
+  AUR_CHECK_CTX(ctx);
+  if (int rc = check_common(ctx, b, t, n_head, d_head, ld_qkv, ld_out)) return rc;
+  if (!q || !k || !v || !out || !lse) return aur::set_error(ctx, AUR_EINVAL, "mha_fwd: null pointer");
+  if (!al16(q) || !al16(k) || !al16(v) || !al16(out))
+    return aur::set_error(ctx, AUR_EINVAL, "mha_fwd: tensors must be 16-byte aligned");
+  AttnArgs a{};
+  a.q = q; a.k = k; a.v = v; a.out = out; a.lse = lse;
+  a.ld_qkv = (int)ld_qkv; a.ld_o = (int)ld_out;
+  a.T = (int)t; a.H = (int)n_head;
+  a.scale = 1.0f / sqrtf((float)d_head);
+  switch (d_head) {
+    case 8: launch_fwd<8>(a, (int)b, ctx->stream); break;
+    case 16: launch_fwd<16>(a, (int)b, ctx->stream); break;
+    case 32: launch_fwd<32>(a, (int)b, ctx->stream); break;
+    default: launch_fwd<64>(a, (int)b, ctx->stream); break;
+  }
+  AUR_LAUNCH_CHECK(ctx, "mha_fwd_kernel");
+  return 0;
+}
+
+int aur_mha_fwd(aur_ctx* ctx, const float* q, const float* k, const float* v, float* out, float* lse,
+                uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head) {
+  return aur_mha_fwd_ex(ctx, q, k, v, n_head * d_head, out, n_head * d_head, lse, b, t, n_head, d_head);
+}
+
+size_t aur_mha_bwd_ws_bytes(uint32_t b, uint32_t t, uint32_t n_head) {
+  return (size_t)b * t * n_head * sizeof(float);
+}
+
+int aur_mha_bwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v, uint32_t ld_qkv,
+                   const float* out, const float* d_out, uint32_t ld_out, const float* lse, float* dq,
+                   float* dk, float* dv, uint32_t ld_dqkv, float* ws, uint32_t b, uint32_t t,
+                   uint32_t n_head, uint32_t d_head) {
+  AUR_CHECK_CTX(ctx);
+  if (int rc = check_common(ctx, b, t, n_head, d_head, ld_qkv, ld_out)) return rc;
+  if (ld_dqkv < n_head * d_head || (ld_dqkv & 3))
+    return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: bad gradient row stride %u", ld_dqkv);
+  if (!q || !k || !v || !out || !d_out || !lse || !dq || !dk || !dv || !ws)
+    return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: null pointer");
+  if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(d_out) || !al16(dq) || !al16(dk) ||
+      !al16(dv) || !al16(ws))
+    return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: tensors must be 16-byte aligned");
+  AttnArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = out; a.dO = d_out; a.lse = const_cast<float*>(lse);
+  a.D = ws; a.dq = dq; a.dk = dk; a.dv = dv;
+  a.ld_qkv = (int)ld_qkv; a.ld_o = (int)ld_out; a.ld_d = (int)ld_dqkv;
+  a.T = (int)t; a.H = (int)n_head;
+  a.scale = 1.0f / sqrtf((float)d_head);
+  switch (d_head) {
+    case 8: launch_bwd<8>(a, (int)b, ctx->stream); break;
+    case 16: launch_bwd<16>(a, (int)b, ctx->stream); break;
+    case 32: launch_bwd<32>(a, (int)b, ctx->stream); break;
+    default: launch_bwd<64>(a, (int)b, ctx->stream); break;
+  }
+  AUR_LAUNCH_CHECK(ctx, "mha_bwd kernels");
+  return 0;
+}
+
+int aur_mha_bwd(aur_ctx* ctx, const float* q, const float* k, const float* v, const float* out,
+                const float* lse, const float* d_out, float* dq, float* dk, float* dv, float* ws,
+                uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head) {
+  const uint32_t d = n_head * d_head;
+  return aur_mha_bwd_ex(ctx, q, k, v, d, out, d_out, d, lse, dq, dk, dv, d, ws, b, t, n_head, d_head);
+}
+
+}  // extern "C"

@@ -1,0 +1,64 @@
+// Internal definitions shared by the HIP translation units of libaurora_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/aurora_hip.h"
+
+// The context: one device, one default-priority stream, and a grow-only
+// workspace used by kernels that need scratch beyond the caller's tensors
+// (split-K partial sums).  The workspace is allocated on first need and kept.
+struct aur_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int cu_count = 0;
+  std::string last_error;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
+namespace aur {
+
+int set_error(aur_ctx* ctx, int code, const char* fmt, ...);
+
+// Makes `ctx` own at least `bytes` of workspace; returns 0 or an error code.
+int ensure_workspace(aur_ctx* ctx, size_t bytes);
+
+}  // namespace aur
+
+#define AUR_CHECK_CTX(ctx)                                   \
+  do {                                                       \
+    if ((ctx) == nullptr) return AUR_EINVAL;                 \
+  } while (0)
+
+// Records a failing HIP call in the context and returns its code.
+#define AUR_HIP(ctx, expr)                                                     \
+  do {                                                                         \
+    hipError_t _e = (expr);                                                    \
+    if (_e != hipSuccess)                                                      \
+      return aur::set_error((ctx), (int)_e, "%s: %s", #expr,                   \
+                            hipGetErrorString(_e));                            \
+  } while (0)
+
+// Checks the launch that was just enqueued.
+#define AUR_LAUNCH_CHECK(ctx, name)                                            \
+  do {                                                                         \
+    hipError_t _e = hipGetLastError();                                         \
+    if (_e != hipSuccess)                                                      \
+      return aur::set_error((ctx), (int)_e, "launch %s: %s", (name),           \
+                            hipGetErrorString(_e));                            \
+  } while (0)
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_16x16x4_f32: D(16x16) += A(16x4)·B(4x16) for one wave.
+// Lane l supplies A[l%16][l/16] and B[l/16][l%16]; it receives
+// D[4*(l/16)+i][l%16] in element i of the result.
+__device__ __forceinline__ floatx4 mfma16x16x4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}

@@ -1,0 +1,420 @@
+// fp32 GEMM family on gfx950 matrix cores (v_mfma_f32_16x16x4_f32).
+//
+// One kernel template covers the three forms of the reference:
+//   A@B   (GemmKernel, src/gpu/matmul.rs:21-120)            A k-contiguous, B n-contiguous
+//   A@Bᵀ  (GemmTransposeBKernel, src/gpu/matmul.rs:122-219)  A k-contiguous, B k-contiguous
+//   dest += dYᵀ·X  (OuterProductAccumKernel, src/gpu/reduce.rs:15-115)
+//                                                           A m-contiguous, B n-contiguous
+// Operands are copied global→LDS exactly as they lie in memory (float4 loads,
+// no transposition); the fragment read adapts instead:
+//   * a k-contiguous operand is read as one float4 along k per lane, and the
+//     four values feed four consecutive MFMAs;
+//   * a k-strided operand is read as four b32 values at rows k, k+1, k+2, k+3.
+// Both operands use the same k permutation inside a 16-wide k chunk: MFMA s
+// (0..3) takes k = 16c + 4·(lane/16) + s, so Σ over s and the MFMA's own
+// 4-wide reduction covers the chunk exactly once.
+//
+// Work split: a 256-thread block (4 waves in 2×2) owns a BM×BN tile; each
+// wave owns (BM/2)×(BN/2) as a grid of 16×16 MFMA tiles.  Global→LDS is
+// double-buffered with one barrier per BK step.  Long-K/small-output shapes
+// (the weight-gradient accumulate) split K over blockIdx.z into fp32 partial
+// tiles that a second kernel reduces in fixed split order — deterministic,
+// no atomics — and adds into the destination.
+#include "common.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct GemmArgs {
+  const float* A;
+  const float* B;
+  float* C;
+  float* P;  // split-K partials [splits][M][N]
+  int M, N, K;
+  int lda, ldb, ldc;
+  int k_chunk;  // K range per blockIdx.z (multiple of BK)
+  int mode;     // 0: C = AB, 1: C += AB, 2: P[z] = partial AB
+  int tiles_m, tiles_n;
+};
+
+template <int BM, int BN, int BK, bool AK, bool BKC>
+struct Smem {
+  // k-contiguous operand: [rows][BK+4]; k-strided operand: [BK][cols+4].
+  static constexpr int A_ELEMS = AK ? BM * (BK + 4) : BK * (BM + 4);
+  static constexpr int B_ELEMS = BKC ? BN * (BK + 4) : BK * (BN + 4);
+  static constexpr int STAGE = A_ELEMS + B_ELEMS;
+  static constexpr int BYTES = 2 * STAGE * 4;
+};
+
+// Loads the (rows × BK) tile of a k-contiguous operand X(r,k)=x[r*ld+k], or
+// the (BK × cols) tile of a k-strided operand X(r,k)=x[k*ld+r], into registers.
+template <int ROWS, int BK, bool KCONTIG, bool VEC>
+struct TileLoader {
+  static constexpr int NV = ROWS * BK / 4 / kThreads;  // float4 per thread
+  static_assert(NV >= 1 && ROWS * BK % (4 * kThreads) == 0, "tile/threads mismatch");
+  floatx4 v[NV];
+
+  __device__ __forceinline__ void load(const float* __restrict__ x, int ld, int r0, int rmax,
+                                       int k0, int kmax, int tid) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int f = tid + i * kThreads;
+      int r, k;
+      if (KCONTIG) {
+        r = f / (BK / 4);
+        k = (f % (BK / 4)) * 4;
+      } else {
+        k = f / (ROWS / 4);
+        r = (f % (ROWS / 4)) * 4;
+      }
+      const int gr = r0 + r, gk = k0 + k;
+      floatx4 val = {0.f, 0.f, 0.f, 0.f};
+      if (KCONTIG) {
+        if (gr < rmax) {
+          const float* p = x + (size_t)gr * ld + gk;
+          if (VEC) {
+            if (gk < kmax) val = *reinterpret_cast<const floatx4*>(p);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (gk + e < kmax) val[e] = p[e];
+          }
+        }
+      } else {
+        if (gk < kmax) {
+          const float* p = x + (size_t)gk * ld + gr;
+          if (VEC) {
+            if (gr < rmax) val = *reinterpret_cast<const floatx4*>(p);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (gr + e < rmax) val[e] = p[e];
+          }
+        }
+      }
+      v[i] = val;
+    }
+  }
+
+  __device__ __forceinline__ void store(float* __restrict__ s, int tid) const {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int f = tid + i * kThreads;
+      int off;
+      if (KCONTIG) {
+        off = (f / (BK / 4)) * (BK + 4) + (f % (BK / 4)) * 4;
+      } else {
+        off = (f / (ROWS / 4)) * (ROWS + 4) + (f % (ROWS / 4)) * 4;
+      }
+      *reinterpret_cast<floatx4*>(s + off) = v[i];
+    }
+  }
+};
+
+// Fragment of one 16-row slice for k chunk c: f[s] is this lane's operand of
+// MFMA s, i.e. X(row0 + lane%16, 16c + 4·(lane/16) + s).
+template <int ROWS, int BK, bool KCONTIG>
+__device__ __forceinline__ floatx4 read_frag(const float* __restrict__ s, int row, int c, int g) {
+  floatx4 f;
+  if (KCONTIG) {
+    f = *reinterpret_cast<const floatx4*>(s + row * (BK + 4) + 16 * c + 4 * g);
+  } else {
+    const float* p = s + (16 * c + 4 * g) * (ROWS + 4) + row;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[e] = p[e * (ROWS + 4)];
+  }
+  return f;
+}
+
+template <int BM, int BN, int BK, bool AK, bool BKC, bool VEC>
+__global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
+  using S = Smem<BM, BN, BK, AK, BKC>;
+  constexpr int WM = BM / 2, WN = BN / 2;  // wave tile
+  constexpr int TM = WM / 16, TN = WN / 16;
+  __shared__ __attribute__((aligned(16))) float smem[2 * S::STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int g16 = lane >> 4, l16 = lane & 15;
+
+  // XCD-aware tile order: consecutive workgroups are dispatched round-robin
+  // over the 8 XCDs; give each XCD a contiguous run of tiles so that tiles
+  // sharing an A row panel hit the same L2.
+  const int ntiles = g.tiles_m * g.tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int tm = pid / g.tiles_n, tn = pid % g.tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int kbeg = blockIdx.z * g.k_chunk;
+  const int kend = min(g.K, kbeg + g.k_chunk);
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+
+  TileLoader<BM, BK, AK, VEC> la;
+  TileLoader<BN, BK, BKC, VEC> lb;
+
+  floatx4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  if (nk > 0) {
+    la.load(g.A, g.lda, m0, g.M, kbeg, kend, tid);
+    lb.load(g.B, g.ldb, n0, g.N, kbeg, kend, tid);
+    la.store(smem, tid);
+    lb.store(smem + S::A_ELEMS, tid);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      const int k0 = kbeg + (kt + 1) * BK;
+      la.load(g.A, g.lda, m0, g.M, k0, kend, tid);
+      lb.load(g.B, g.ldb, n0, g.N, k0, kend, tid);
+    }
+    const float* sa = smem + cur * S::STAGE;
+    const float* sb = sa + S::A_ELEMS;
+#pragma unroll
+    for (int c = 0; c < BK / 16; ++c) {
+      floatx4 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = read_frag<BM, BK, AK>(sa, wm * WM + i * 16 + l16, c, g16);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = read_frag<BN, BK, BKC>(sb, wn * WN + j * 16 + l16, c, g16);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x4(fa[i][s], fb[j][s], acc[i][j]);
+    }
+    if (more) {
+      float* na = smem + (cur ^ 1) * S::STAGE;
+      la.store(na, tid);
+      lb.store(na + S::A_ELEMS, tid);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds D[4·g16 + e][l16] of each 16×16 tile.
+  float* out;
+  int ldo;
+  if (g.mode == 2) {
+    out = g.P + (size_t)blockIdx.z * g.M * g.N;
+    ldo = g.N;
+  } else {
+    out = g.C;
+    ldo = g.ldc;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * WN + j * 16 + l16;
+      if (col >= g.N) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = m0 + wm * WM + i * 16 + 4 * g16 + e;
+        if (row < g.M) {
+          float* p = out + (size_t)row * ldo + col;
+          if (g.mode == 1)
+            *p += acc[i][j][e];
+          else
+            *p = acc[i][j][e];
+        }
+      }
+    }
+  }
+}
+
+// C(m,n) (+)= Σ_{z=0..splits-1} P[z][m][n], summed in increasing z.
+__global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ P, float* __restrict__ C,
+                                                      int M, int N, int ldc, int splits,
+                                                      int accumulate) {
+  const size_t total = (size_t)M * N;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    float s = P[i];
+    for (int z = 1; z < splits; ++z) s += P[(size_t)z * total + i];
+    const size_t row = i / N, col = i % N;
+    float* c = C + row * ldc + col;
+    *c = accumulate ? *c + s : s;
+  }
+}
+
+struct Plan {
+  int bm, bn, splits, k_chunk;
+};
+
+constexpr int kBK = 32;
+
+Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split) {
+  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  Plan p{128, 128, 1, K};
+  if (tiles(128, 128) >= cus) {
+    p = {128, 128, 1, K};
+  } else if (tiles(128, 64) >= cus) {
+    p = {128, 64, 1, K};
+  } else {
+    p = {64, 64, 1, K};
+    if (tiles(128, 128) * 4 >= cus && K >= 2048) p = {128, 128, 1, K};
+  }
+  if (allow_split) {
+    const int t = tiles(p.bm, p.bn);
+    int splits = 1;
+    while (t * splits < cus && K / (splits * 2) >= 256) splits *= 2;
+    if (splits > 1) {
+      int chunk = (K + splits - 1) / splits;
+      chunk = (chunk + kBK - 1) / kBK * kBK;
+      p.splits = (K + chunk - 1) / chunk;
+      p.k_chunk = chunk;
+    }
+  }
+  // Tuning override: AUR_GEMM_CFG="BMxBN[:splits]".
+  if (const char* env = std::getenv("AUR_GEMM_CFG")) {
+    int bm = 0, bn = 0, sp = 1;
+    if (std::sscanf(env, "%dx%d:%d", &bm, &bn, &sp) >= 2 &&
+        ((bm == 128 && bn == 128) || (bm == 128 && bn == 64) || (bm == 64 && bn == 64))) {
+      p.bm = bm;
+      p.bn = bn;
+      if (!allow_split) sp = 1;
+      sp = std::max(1, sp);
+      int chunk = (K + sp - 1) / sp;
+      chunk = (chunk + kBK - 1) / kBK * kBK;
+      p.splits = std::max(1, (K + chunk - 1) / chunk);
+      p.k_chunk = chunk;
+    }
+  }
+  return p;
+}
+
+template <int BM, int BN, bool AK, bool BKC>
+void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st) {
+  dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
+  if (vec)
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, kBK, AK, BKC, true>), grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, kBK, AK, BKC, false>), grid, dim3(kThreads), 0, st, a);
+}
+
+template <bool AK, bool BKC>
+void launch_layout(const GemmArgs& a, const Plan& p, bool vec, hipStream_t st) {
+  if (p.bm == 128 && p.bn == 128)
+    launch_tile<128, 128, AK, BKC>(a, p.splits, vec, st);
+  else if (p.bm == 128 && p.bn == 64)
+    launch_tile<128, 64, AK, BKC>(a, p.splits, vec, st);
+  else
+    launch_tile<64, 64, AK, BKC>(a, p.splits, vec, st);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+namespace aur {
+
+// C (+)= op(A)·op(B) on ctx's stream.  See aur_gemm_ex for operand meaning.
+int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
+         int ldb, float* C, int ldc, int M, int N, int K, bool accumulate) {
+  if (M < 0 || N < 0 || K < 0) return set_error(ctx, AUR_EINVAL, "gemm: negative dims");
+  if (M == 0 || N == 0) return 0;
+  if (!C || (K > 0 && (!A || !B))) return set_error(ctx, AUR_EINVAL, "gemm: null pointer");
+  if (K == 0) {
+    if (!accumulate) {
+      for (int r = 0; r < M; ++r)
+        AUR_HIP(ctx, hipMemsetAsync(C + (size_t)r * ldc, 0, sizeof(float) * N, ctx->stream));
+    }
+    return 0;
+  }
+  // The A / B "row" extents (the contiguous index of a k-strided operand).
+  const int a_rows = M, b_rows = N;
+  const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
+                   (a_kcontig ? (K % 4 == 0) : (a_rows % 4 == 0)) &&
+                   (b_kcontig ? (K % 4 == 0) : (b_rows % 4 == 0));
+  // Split-K only pays for long K with few output tiles; used for every form.
+  Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/true);
+  GemmArgs a{};
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.tiles_m = (M + p.bm - 1) / p.bm;
+  a.tiles_n = (N + p.bn - 1) / p.bn;
+  a.k_chunk = p.k_chunk;
+  if (p.splits > 1) {
+    const size_t need = (size_t)p.splits * M * N * sizeof(float);
+    int rc = ensure_workspace(ctx, need);
+    if (rc) return rc;
+    a.P = static_cast<float*>(ctx->ws);
+    a.mode = 2;
+  } else {
+    a.mode = accumulate ? 1 : 0;
+  }
+  if (a_kcontig && b_kcontig)
+    launch_layout<true, true>(a, p, vec, ctx->stream);
+  else if (a_kcontig && !b_kcontig)
+    launch_layout<true, false>(a, p, vec, ctx->stream);
+  else if (!a_kcontig && b_kcontig)
+    launch_layout<false, true>(a, p, vec, ctx->stream);
+  else
+    launch_layout<false, false>(a, p, vec, ctx->stream);
+  AUR_LAUNCH_CHECK(ctx, "gemm_f32_mfma");
+  if (p.splits > 1) {
+    const size_t total = (size_t)M * N;
+    int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, a.P, C, M, N, ldc,
+                       p.splits, accumulate ? 1 : 0);
+    AUR_LAUNCH_CHECK(ctx, "splitk_reduce");
+  }
+  return 0;
+}
+
+}  // namespace aur
+
+extern "C" {
+
+int aur_gemm_nn(aur_ctx* ctx, const float* a, const float* b, float* c, uint32_t m, uint32_t n,
+                uint32_t k) {
+  AUR_CHECK_CTX(ctx);
+  return aur::gemm(ctx, true, false, a, (int)k, b, (int)n, c, (int)n, (int)m, (int)n, (int)k, false);
+}
+
+int aur_gemm_nt(aur_ctx* ctx, const float* a, const float* b, float* c, uint32_t m, uint32_t n,
+                uint32_t k) {
+  AUR_CHECK_CTX(ctx);
+  return aur::gemm(ctx, true, true, a, (int)k, b, (int)k, c, (int)n, (int)m, (int)n, (int)k, false);
+}
+
+int aur_outer_accum(aur_ctx* ctx, const float* x, const float* d_y, float* dest, uint32_t d_out,
+                    uint32_t d_in, uint32_t t) {
+  AUR_CHECK_CTX(ctx);
+  // dest(o,i) += Σ_t A(o,t)·B(t,i) with A(o,t) = d_y[t*d_out + o] (k-strided)
+  // and B(t,i) = x[t*d_in + i] (k-strided).
+  return aur::gemm(ctx, false, false, d_y, (int)d_out, x, (int)d_in, dest, (int)d_in, (int)d_out,
+                   (int)d_in, (int)t, true);
+}
+
+int aur_gemm_ex(aur_ctx* ctx, int a_kcontig, int b_kcontig, const float* a, uint32_t lda,
+                const float* b, uint32_t ldb, float* c, uint32_t ldc, uint32_t m, uint32_t n,
+                uint32_t k, int accumulate) {
+  AUR_CHECK_CTX(ctx);
+  return aur::gemm(ctx, a_kcontig != 0, b_kcontig != 0, a, (int)lda, b, (int)ldb, c, (int)ldc,
+                   (int)m, (int)n, (int)k, accumulate != 0);
+}
+
+}  // extern "C"

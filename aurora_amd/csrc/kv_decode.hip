@@ -1,0 +1,218 @@
+// KV-cache decode attention: one new query per (sequence, head) against the
+// cached K/V rows [0, t_total).  Reference: MhaKvCacheKernel
+// (src/gpu/kv_cache.rs:247-351) and the CPU block_step attention
+// (src/transformer/kv_cache.rs:181-219): s_j = q·k_j/sqrt(d_head),
+// p = softmax(s), out = Σ_j p_j v_j.
+//
+// The work is HBM-bound (every cached K and V row is read once per step), so
+// the kernel is shaped for memory-level parallelism rather than math:
+//   * the key axis is split into chunks of KC keys; one 256-thread block per
+//     (chunk, head, sequence) — thousands of blocks at the decode shapes;
+//   * d_head/4 lanes cover one K/V row of a head with float4 loads (256
+//     contiguous bytes at d_head = 64, 4 keys per wave load instruction);
+//   * each block writes its chunk's (row max, row sum, unnormalised output);
+//     a second kernel merges the chunks of a (sequence, head) in increasing
+//     chunk order — a fixed order, so the result is deterministic.
+#include "common.hpp"
+
+namespace {
+
+constexpr int DHMAX = 64;
+constexpr int KC = 128;              // keys per chunk (block)
+constexpr int KPW = KC / 4;          // keys per wave
+constexpr int PART = 4 + DHMAX;      // per-chunk record: m, l, pad, pad, o[d_head]
+constexpr float LOG2E = 1.4426950408889634f;
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+struct KvArgs {
+  const float* q;       // [B, ld] rows, head h at h*d_head
+  const float* kh;      // [B, max_len, ld]
+  const float* vh;
+  float* out;           // [B, ld]
+  float* ws;            // [B, H, nch, PART]
+  const int32_t* t_dev; // per-sequence lengths (device) or null
+  int t_scalar;         // length when t_dev is null
+  int ld;               // row stride (= n_head * d_head)
+  int max_len;
+  int H;
+  int nch;
+  float scale;
+};
+
+// DH/4 lanes cover one K/V row (LPK), so one wave load instruction covers
+// KPS = 64/LPK keys.
+template <int DH>
+__global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
+  constexpr int LPK = DH / 4, KPS = 64 / LPK;
+  __shared__ float sc[KC];
+  __shared__ float red[4];
+  __shared__ __attribute__((aligned(16))) float obuf[4][DH];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane / LPK, part = lane % LPK;
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int T = a.t_dev ? a.t_dev[b] : a.t_scalar;
+  const int c0 = c * KC;
+  float* rec = a.ws + (((size_t)b * a.H + h) * a.nch + c) * PART;
+  if (c0 >= T) {  // chunk past this sequence's end: neutral record
+    if (tid < PART) rec[tid] = tid == 0 ? -INFINITY : 0.f;
+    return;
+  }
+  const size_t hist = (size_t)b * a.max_len;
+  floatx4 qv = *reinterpret_cast<const floatx4*>(a.q + (size_t)b * a.ld + h * DH + 4 * part);
+  qv *= a.scale * LOG2E;
+
+  // Scores of this wave's keys, KPS per step (one per LPK-lane group).
+  float s_loc[KPW / KPS];
+#pragma unroll
+  for (int it = 0; it < KPW / KPS; ++it) {
+    const int key = c0 + w * KPW + KPS * it + g;
+    float s = 0.f;
+    if (key < T) {
+      const floatx4 kv = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + h * DH + 4 * part);
+      s = qv[0] * kv[0] + qv[1] * kv[1] + qv[2] * kv[2] + qv[3] * kv[3];
+    }
+    s_loc[it] = s;
+  }
+#pragma unroll
+  for (int it = 0; it < KPW / KPS; ++it) {
+    float s = s_loc[it];
+#pragma unroll
+    for (int m = LPK / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
+    const int kl = w * KPW + KPS * it + g;
+    if (part == 0) sc[kl] = (c0 + kl < T) ? s : -INFINITY;
+  }
+  __syncthreads();
+
+  // Chunk max and exp-sum (log2 domain).
+  float v = tid < KC ? sc[tid] : -INFINITY;
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, shfl_xor(v, o));
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float e = 0.f;
+  if (tid < KC) {
+    e = exp2f(sc[tid] - M);
+    sc[tid] = e;
+  }
+  float sum = e;
+  for (int o = 32; o >= 1; o >>= 1) sum += shfl_xor(sum, o);
+  if (lane == 0) red[w] = sum;
+  __syncthreads();
+  const float L = (red[0] + red[1]) + (red[2] + red[3]);
+
+  // Unnormalised Σ_j p_j v_j over this wave's keys, 4 dims per lane.
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int it = 0; it < KPW / KPS; ++it) {
+    const int kl = w * KPW + KPS * it + g;
+    const int key = c0 + kl;
+    if (key < T) {
+      const floatx4 vv = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + h * DH + 4 * part);
+      acc += sc[kl] * vv;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int m = LPK; m < 64; m <<= 1) acc[i] += shfl_xor(acc[i], m);
+  if (g == 0) *reinterpret_cast<floatx4*>(&obuf[w][4 * part]) = acc;
+  __syncthreads();
+  if (tid < DH) {
+    rec[4 + tid] = (obuf[0][tid] + obuf[1][tid]) + (obuf[2][tid] + obuf[3][tid]);
+    if (tid == 0) {
+      rec[0] = M;
+      rec[1] = L;
+    }
+  }
+}
+
+// out[b, h*DH + d] = Σ_c 2^(m_c − M) o_c[d] / Σ_c 2^(m_c − M) l_c, c ascending.
+template <int DH>
+__global__ void __launch_bounds__(64) kv_combine_kernel(KvArgs a) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const float* rec = a.ws + ((size_t)b * a.H + h) * a.nch * PART;
+  float M = -INFINITY;
+  for (int c = 0; c < a.nch; ++c) M = fmaxf(M, rec[c * PART]);
+  float L = 0.f, o = 0.f;
+  for (int c = 0; c < a.nch; ++c) {
+    const float f = exp2f(rec[c * PART] - M);
+    L += f * rec[c * PART + 1];
+    o += f * rec[c * PART + 4 + d];
+  }
+  a.out[(size_t)b * a.ld + h * DH + d] = L > 0.f ? o / L : 0.f;
+}
+
+// Launches ceil(t_max / KC) chunks per (head, sequence); t_max must be at
+// least every sequence's length (a shorter sequence's surplus chunks write
+// neutral records).  The scratch records are laid out [B][H][nch].
+template <int DH>
+void launch_dh(const KvArgs& a, int B, hipStream_t st) {
+  dim3 g1(a.nch, a.H, B);
+  hipLaunchKernelGGL(kv_chunk_kernel<DH>, g1, dim3(256), 0, st, a);
+  dim3 g2(a.H, B);
+  hipLaunchKernelGGL(kv_combine_kernel<DH>, g2, dim3(DH), 0, st, a);
+}
+
+int launch(aur_ctx* ctx, KvArgs& a, int B, int t_max, int d_head) {
+  a.nch = (t_max + KC - 1) / KC;
+  switch (d_head) {
+    case 8: launch_dh<8>(a, B, ctx->stream); break;
+    case 16: launch_dh<16>(a, B, ctx->stream); break;
+    case 32: launch_dh<32>(a, B, ctx->stream); break;
+    default: launch_dh<64>(a, B, ctx->stream); break;
+  }
+  AUR_LAUNCH_CHECK(ctx, "kv decode kernels");
+  return 0;
+}
+
+bool dh_ok(uint32_t d) { return d == 8 || d == 16 || d == 32 || d == 64; }
+
+}  // namespace
+
+extern "C" {
+
+size_t aur_mha_kv_ws_bytes(uint32_t b, uint32_t n_head, uint32_t max_len) {
+  return (size_t)b * n_head * ((max_len + KC - 1) / KC) * PART * sizeof(float);
+}
+
+int aur_mha_kv_step(aur_ctx* ctx, const float* q_new, const float* k_history, const float* v_history,
+                    float* out, float* scratch, uint32_t t_total, uint32_t n_head, uint32_t d_head,
+                    uint32_t max_len) {
+  AUR_CHECK_CTX(ctx);
+  if (!dh_ok(d_head))
+    return aur::set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%u, supports 8/16/32/64", d_head);
+  if (t_total == 0 || t_total > max_len || n_head == 0)
+    return aur::set_error(ctx, AUR_EINVAL, "mha_kv_step: t_total=%u max_len=%u", t_total, max_len);
+  if (!q_new || !k_history || !v_history || !out || !scratch)
+    return aur::set_error(ctx, AUR_EINVAL, "mha_kv_step: null pointer");
+  KvArgs a{};
+  a.q = q_new; a.kh = k_history; a.vh = v_history; a.out = out; a.ws = scratch;
+  a.t_dev = nullptr; a.t_scalar = (int)t_total;
+  a.ld = (int)(n_head * d_head); a.max_len = (int)max_len; a.H = (int)n_head;
+  a.scale = 1.0f / sqrtf((float)d_head);
+  return launch(ctx, a, 1, (int)t_total, (int)d_head);
+}
+
+int aur_mha_kv_step_batched(aur_ctx* ctx, const float* q_new, const float* k_history,
+                            const float* v_history, float* out, float* scratch, const int32_t* t_total,
+                            uint32_t t_max, uint32_t b, uint32_t n_head, uint32_t d_head,
+                            uint32_t max_len) {
+  AUR_CHECK_CTX(ctx);
+  if (!dh_ok(d_head))
+    return aur::set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%u, supports 8/16/32/64", d_head);
+  if (b == 0 || n_head == 0 || t_max == 0 || t_max > max_len)
+    return aur::set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: b=%u t_max=%u max_len=%u", b, t_max,
+                          max_len);
+  if (!q_new || !k_history || !v_history || !out || !scratch || !t_total)
+    return aur::set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: null pointer");
+  KvArgs a{};
+  a.q = q_new; a.kh = k_history; a.vh = v_history; a.out = out; a.ws = scratch;
+  a.t_dev = t_total; a.t_scalar = 0;
+  a.ld = (int)(n_head * d_head); a.max_len = (int)max_len; a.H = (int)n_head;
+  a.scale = 1.0f / sqrtf((float)d_head);
+  return launch(ctx, a, (int)b, (int)t_max, (int)d_head);
+}
+
+}  // extern "C"

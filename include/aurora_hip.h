@@ -1,0 +1,179 @@
+/*
+ * aurora_hip.h — C ABI of libaurora_hip.so, the MI355X (gfx950) backend for
+ * Aurora's matrix-multiply / causal-attention hot path.
+ *
+ * Conventions (all entry points):
+ *   - every function returns int: 0 = success, otherwise a hipError_t value or
+ *     one of the AUR_E* codes below; aur_last_error(ctx) gives the message.
+ *   - every pointer argument that names a tensor is a DEVICE pointer owned by
+ *     the caller (allocated with aur_malloc or any other HIP allocator); the
+ *     launchers never allocate tensors.  Tensors are fp32 row-major, token ids
+ *     and lengths are 32-bit.
+ *   - all work of one context is ordered on that context's single HIP stream;
+ *     launchers only enqueue (no host sync) — like the reference's
+ *     `dispatch_into`, which only records into a wgpu::CommandEncoder.
+ *     aur_d2h and aur_sync are the synchronising calls.
+ *   - a context is not thread-safe; callers serialise access to it (the
+ *     reference's GpuContext likewise wraps one queue).
+ *
+ * Weights follow the reference layout [d_out, d_in] (src/attention.rs:162-167),
+ * so a forward linear is y = x·Wᵀ (aur_gemm_nt).
+ */
+#ifndef AURORA_HIP_H
+#define AURORA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct aur_ctx aur_ctx;
+
+#define AUR_OK 0
+/* Library-level error codes sit above the hipError_t range. */
+#define AUR_EINVAL 10001   /* bad argument (shape, null pointer, alignment) */
+#define AUR_ENOMEM 10002   /* workspace could not be obtained */
+#define AUR_ELIMIT 10003   /* shape exceeds a documented kernel limit */
+
+/* ---- context / runtime (replaces src/gpu/context.rs:22-69 GpuContext::new
+ *      and src/gpu/buffers.rs:27-191 GpuBuffer) ------------------------- */
+
+/* Create a context on HIP device `device` with one default-priority stream.
+ * Mirrors GpuContext::new() -> Result<Self, GpuInitError> (context.rs:22):
+ * the only fallible constructor; non-zero when no usable gfx950 device. */
+int aur_init(int device, aur_ctx** out);
+int aur_destroy(aur_ctx* ctx);
+/* Message of the last failing call on this context ("" if none). ctx may be
+ * NULL, then the message of the last aur_init failure is returned. */
+const char* aur_last_error(const aur_ctx* ctx);
+/* The context's stream (a hipStream_t) for callers that interoperate. */
+void* aur_stream(aur_ctx* ctx);
+/* Device name + arch, e.g. "AMD Instinct MI355X gfx950:sramecc+:xnack-". */
+int aur_device_info(aur_ctx* ctx, char* buf, size_t len, int* cu_count);
+
+/* Memory: GpuBuffer::{empty,zeros,from_slice,upload,download}
+ * (buffers.rs:27-191).  aur_d2h blocks until the copy is done, like
+ * GpuBuffer::download (map_async + poll(Wait)). */
+int aur_malloc(aur_ctx* ctx, size_t bytes, void** out);
+int aur_free(aur_ctx* ctx, void* ptr);
+int aur_h2d(aur_ctx* ctx, void* dst, const void* src, size_t bytes);
+int aur_d2h(aur_ctx* ctx, void* dst, const void* src, size_t bytes);
+int aur_d2d(aur_ctx* ctx, void* dst, const void* src, size_t bytes);
+int aur_memset0(aur_ctx* ctx, void* dst, size_t bytes);
+int aur_sync(aur_ctx* ctx);
+
+/* Timing on the context's stream (replaces the reference's wgpu
+ * timestamp-query GpuProfiler mark/resolve, src/gpu/profiler.rs:13-138).
+ * aur_event_elapsed_ms waits for `stop` and returns stop − start in ms. */
+int aur_event_create(aur_ctx* ctx, void** ev);
+int aur_event_record(aur_ctx* ctx, void* ev);
+int aur_event_elapsed_ms(aur_ctx* ctx, void* start, void* stop, float* ms);
+int aur_event_destroy(aur_ctx* ctx, void* ev);
+
+/* ---- GEMM family --------------------------------------------------------- */
+
+/* C[m,n] = A[m,k] · B[k,n]   (overwrite).
+ * Replaces GemmKernel::dispatch_into(ctx, enc, a, b, c, m, n, k)
+ * (src/gpu/matmul.rs:285-321; WGSL GEMM_WGSL matmul.rs:21-120). */
+int aur_gemm_nn(aur_ctx* ctx, const float* a, const float* b, float* c,
+                uint32_t m, uint32_t n, uint32_t k);
+
+/* C[m,n] = Σ_k A[m,k] · B[n,k]   (overwrite) — every forward linear y = x·Wᵀ
+ * and the tied LM head.
+ * Replaces GemmTransposeBKernel::dispatch_into(ctx, enc, a, b, c, m, n, k)
+ * (src/gpu/matmul.rs:371-383; WGSL matmul.rs:122-219). */
+int aur_gemm_nt(aur_ctx* ctx, const float* a, const float* b, float* c,
+                uint32_t m, uint32_t n, uint32_t k);
+
+/* dest[d_out,d_in] += Σ_t d_y[t,d_out] · x[t,d_in]   (read-modify-write,
+ * deterministic, no atomics: a split over t is reduced in a fixed order).
+ * Replaces OuterProductAccumKernel::dispatch_into(ctx, enc, x, d_y, dest,
+ * d_out, d_in, t) (src/gpu/reduce.rs:176-207; WGSL reduce.rs:15-115). */
+int aur_outer_accum(aur_ctx* ctx, const float* x, const float* d_y, float* dest,
+                    uint32_t d_out, uint32_t d_in, uint32_t t);
+
+/* General strided form used by the model orchestrator (no reference
+ * counterpart as one call: it is the union of the three kernels above with
+ * explicit leading dimensions).
+ *   a_kcontig != 0 : A(m,k) = a[m*lda + k]   else A(m,k) = a[k*lda + m]
+ *   b_kcontig != 0 : B(k,n) = b[n*ldb + k]   else B(k,n) = b[k*ldb + n]
+ *   C(m,n) = c[m*ldc + n];  accumulate != 0 → C += A·B  else C = A·B. */
+int aur_gemm_ex(aur_ctx* ctx, int a_kcontig, int b_kcontig,
+                const float* a, uint32_t lda, const float* b, uint32_t ldb,
+                float* c, uint32_t ldc, uint32_t m, uint32_t n, uint32_t k,
+                int accumulate);
+
+/* ---- causal multi-head attention ----------------------------------------- */
+
+/* Forward for a batch of `b` sequences: q,k,v,out are [b*t, n_head*d_head]
+ * (head h at column offset h*d_head, the reference's per-sequence layout
+ * with a leading batch axis); scale = 1/sqrt(d_head), causal mask j > i.
+ * `lse` [b, n_head, t] receives each row's log-sum-exp of the scaled scores;
+ * it takes the slot of the reference's `probs` [n_head,t,t], which no caller
+ * reads back (it is only the forward→backward hand-off).
+ * Replaces CausalMhaForwardKernel::dispatch_into(ctx, enc, q, k, v, out,
+ * probs, t, n_head, d_head) (src/gpu/attention.rs:400-443).
+ * Limits: d_head ∈ {8, 16, 32, 64} (AUR_ELIMIT otherwise); any t >= 1;
+ * q/k/v/out 16-byte aligned. */
+int aur_mha_fwd(aur_ctx* ctx, const float* q, const float* k, const float* v,
+                float* out, float* lse,
+                uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head);
+
+/* Backward: dq, dk, dv are ACCUMULATED (+=), the caller zeroes them first
+ * (attention.rs:575-578).  Deterministic: every output element has exactly
+ * one writer, three passes (row dot D = Σ dO⊙O, dQ over key tiles, dK/dV
+ * over query tiles).  `ws` is a caller-owned workspace of at least
+ * aur_mha_bwd_ws_bytes(b, t, n_head) bytes (takes the slot of the reference's
+ * d_scores_scratch [n_head,t,t]).
+ * Replaces CausalMhaBackwardKernel::dispatch_into(ctx, enc, q, k, v, probs,
+ * d_out, dq, dk, dv, d_scores_scratch, t, n_head, d_head)
+ * (src/gpu/attention.rs:580-685). */
+size_t aur_mha_bwd_ws_bytes(uint32_t b, uint32_t t, uint32_t n_head);
+int aur_mha_bwd(aur_ctx* ctx, const float* q, const float* k, const float* v,
+                const float* out, const float* lse, const float* d_out,
+                float* dq, float* dk, float* dv, float* ws,
+                uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head);
+
+/* Strided forms (row strides in floats) used by the orchestrator to read
+ * q/k/v straight out of a fused [rows, 3*d] QKV projection. */
+int aur_mha_fwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v,
+                   uint32_t ld_qkv, float* out, uint32_t ld_out, float* lse,
+                   uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head);
+int aur_mha_bwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v,
+                   uint32_t ld_qkv, const float* out, const float* d_out,
+                   uint32_t ld_out, const float* lse, float* dq, float* dk,
+                   float* dv, uint32_t ld_dqkv, float* ws,
+                   uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head);
+
+/* ---- KV-cache decode attention --------------------------------------------- */
+
+/* One new query per head against history rows [0, t_total):
+ * q_new [n_head*d_head], k_history/v_history [max_len, n_head*d_head],
+ * out [n_head*d_head].  `scratch` is caller-owned, at least
+ * aur_mha_kv_ws_bytes(1, n_head, max_len) bytes.
+ * Replaces MhaKvCacheKernel::dispatch_into(ctx, enc, q_new, k_history,
+ * v_history, out, scratch, t_total, n_head, d_head, max_len)
+ * (src/gpu/kv_cache.rs:421-465). */
+size_t aur_mha_kv_ws_bytes(uint32_t b, uint32_t n_head, uint32_t max_len);
+int aur_mha_kv_step(aur_ctx* ctx, const float* q_new, const float* k_history,
+                    const float* v_history, float* out, float* scratch,
+                    uint32_t t_total, uint32_t n_head, uint32_t d_head,
+                    uint32_t max_len);
+
+/* Batched form for `b` sequences decoded together: q_new/out [b, d],
+ * k_history/v_history [b, max_len, d], per-sequence lengths in the DEVICE
+ * array t_total[b] (1 <= t_total[i] <= max_len, max over i given as
+ * t_max on the host).  No reference counterpart as one call: the reference
+ * decodes one sequence per call (src/gpu/transformer.rs:2410). */
+int aur_mha_kv_step_batched(aur_ctx* ctx, const float* q_new,
+                            const float* k_history, const float* v_history,
+                            float* out, float* scratch, const int32_t* t_total,
+                            uint32_t t_max, uint32_t b, uint32_t n_head,
+                            uint32_t d_head, uint32_t max_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AURORA_HIP_H */

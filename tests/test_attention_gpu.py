@@ -1,0 +1,195 @@
+"""GPU parity of causal MHA forward / backward and KV-cache decode attention.
+
+Mirrors tests/gpu_parity.rs:217-355 (causal_mha_{forward,backward}_matches_cpu,
+shapes (t,H,dh) ∈ {(4,2,8),(8,4,16),(12,2,32)} and t=6,H=2,dh=8) against the
+CPU restatement, tests/kv_cache.rs:346-386 (t_total = 80 > 64: stride loops),
+then the BASELINE config-2 shape (B16 H8 T1024 dh64) against float64.
+North-star tolerance for attention: 1e-3 (normalised, see parity.py).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests.attn_ref import causal_attention_f64, causal_attention_grad_f64
+from tests.parity import fro_rel, max_norm_rel, max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL_ATTN = 1e-3
+TOL_REF = 5e-2  # tests/gpu_parity.rs:255, :350 (pointwise vs the fp32 CPU path)
+
+
+def _n(rng, n):
+    return rng.standard_normal(n).astype(np.float32)
+
+
+def _fwd(ctx, q, k, v, B, T, H, dh):
+    from aurora_amd.gpu import CausalMhaForwardKernel, GpuBuffer
+
+    bq, bk, bv = (GpuBuffer.from_slice(ctx, x) for x in (q, k, v))
+    out = GpuBuffer.zeros(ctx, B * T * H * dh)
+    lse = GpuBuffer.zeros(ctx, B * H * T)
+    CausalMhaForwardKernel.new(ctx).dispatch_into(ctx, bq, bk, bv, out, lse, T, H, dh, b=B)
+    res = out.download(), lse.download()
+    for x in (bq, bk, bv, out, lse):
+        x.free()
+    return res
+
+
+def _bwd(ctx, q, k, v, o, lse, d_out, B, T, H, dh, init=None):
+    from aurora_amd.gpu import CausalMhaBackwardKernel, GpuBuffer
+
+    n = B * T * H * dh
+    bufs = [GpuBuffer.from_slice(ctx, x) for x in (q, k, v, o, lse, d_out)]
+    if init is None:
+        grads = [GpuBuffer.zeros(ctx, n) for _ in range(3)]
+    else:
+        grads = [GpuBuffer.from_slice(ctx, x) for x in init]
+    ws = GpuBuffer.empty(ctx, CausalMhaBackwardKernel.workspace_len(T, H, B))
+    CausalMhaBackwardKernel.new(ctx).dispatch_into(ctx, *bufs, *grads, ws, T, H, dh, b=B)
+    res = [g.download() for g in grads]
+    for x in bufs + grads + [ws]:
+        x.free()
+    return res
+
+
+@pytest.mark.parametrize("t,H,dh", [(4, 2, 8), (8, 4, 16), (12, 2, 32), (70, 2, 64), (129, 3, 32)])
+def test_causal_mha_forward_matches_cpu(ctx, t, H, dh):
+    rng = np.random.default_rng(0x4274 + t)
+    d = H * dh
+    q, k, v = _n(rng, t * d), _n(rng, t * d), _n(rng, t * d)
+    out, lse = _fwd(ctx, q, k, v, 1, t, H, dh)
+    want, _ = oracle.mha_heads_forward(q, k, v, t, H, dh)
+    assert max_rel_err(out, want) < TOL_REF
+    o64, l64 = causal_attention_f64(*(x.reshape(1, t, H, dh).astype(np.float64) for x in (q, k, v)))
+    assert fro_rel(out, o64) < TOL_ATTN and max_norm_rel(out, o64) < TOL_ATTN
+    np.testing.assert_allclose(lse.reshape(1, H, t), l64, rtol=0, atol=1e-4)
+
+
+@pytest.mark.parametrize("t,H,dh", [(6, 2, 8), (12, 2, 32), (65, 2, 64), (200, 1, 16)])
+def test_causal_mha_backward_matches_cpu(ctx, t, H, dh):
+    """gpu_parity.rs:267-355: dq/dk/dv accumulate into zeroed buffers."""
+    rng = np.random.default_rng(0x5151 + t)
+    d = H * dh
+    q, k, v, do = (_n(rng, t * d) for _ in range(4))
+    out, lse = _fwd(ctx, q, k, v, 1, t, H, dh)
+    dq, dk, dv = _bwd(ctx, q, k, v, out, lse, do, 1, t, H, dh)
+    _, probs = oracle.mha_heads_forward(q, k, v, t, H, dh)
+    wq, wk, wv = oracle.mha_heads_backward(q, k, v, probs, do, t, H, dh)
+    for got, want in ((dq, wq), (dk, wk), (dv, wv)):
+        assert fro_rel(got, want) < TOL_ATTN
+    g64 = causal_attention_grad_f64(*(x.reshape(1, t, H, dh).astype(np.float64) for x in (q, k, v, do)))
+    for got, want in zip((dq, dk, dv), g64):
+        assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
+
+
+def test_backward_accumulates_and_is_deterministic(ctx):
+    B, T, H, dh = 2, 97, 2, 64
+    rng = np.random.default_rng(9)
+    n = B * T * H * dh
+    q, k, v, do = (_n(rng, n) for _ in range(4))
+    init = [_n(rng, n) for _ in range(3)]
+    out, lse = _fwd(ctx, q, k, v, B, T, H, dh)
+    g0 = _bwd(ctx, q, k, v, out, lse, do, B, T, H, dh)
+    g1 = _bwd(ctx, q, k, v, out, lse, do, B, T, H, dh, init=init)
+    g2 = _bwd(ctx, q, k, v, out, lse, do, B, T, H, dh, init=init)
+    for a0, a1, a2, i0 in zip(g0, g1, g2, init):
+        assert np.array_equal(a1, a2)  # bitwise run-to-run
+        np.testing.assert_allclose(a1, i0 + a0, rtol=1e-5, atol=1e-5)
+
+
+def test_causal_future_independence(ctx):
+    """tests/transformer_primitives.rs:179: changing k/v at j > i leaves out[i]."""
+    B, T, H, dh = 1, 150, 2, 64
+    rng = np.random.default_rng(11)
+    n = T * H * dh
+    q, k, v = _n(rng, n), _n(rng, n), _n(rng, n)
+    o1, _ = _fwd(ctx, q, k, v, B, T, H, dh)
+    cut = 77
+    k2, v2 = k.copy(), v.copy()
+    k2[(cut + 1) * H * dh:] = _n(rng, n - (cut + 1) * H * dh)
+    v2[(cut + 1) * H * dh:] = _n(rng, n - (cut + 1) * H * dh)
+    o2, _ = _fwd(ctx, q, k2, v2, B, T, H, dh)
+    m = (cut + 1) * H * dh
+    assert np.array_equal(o1[:m], o2[:m])
+    assert not np.array_equal(o1[m:], o2[m:])
+
+
+def test_config2_mha_fwd_bwd(ctx):
+    """B16 H8 T1024 dh64, N(0,1) seed 1, scale 1/8, causal."""
+    B, T, H, dh = 16, 1024, 8, 64
+    rng = np.random.default_rng(1)
+    n = B * T * H * dh
+    q, k, v, do = (_n(rng, n) for _ in range(4))
+    out, lse = _fwd(ctx, q, k, v, B, T, H, dh)
+    dq, dk, dv = _bwd(ctx, q, k, v, out, lse, do, B, T, H, dh)
+    shp = (B, T, H, dh)
+    q64, k64, v64, do64 = (x.reshape(shp).astype(np.float64) for x in (q, k, v, do))
+    o64, l64 = causal_attention_f64(q64, k64, v64)
+    assert fro_rel(out, o64) < TOL_ATTN and max_norm_rel(out, o64) < TOL_ATTN
+    assert np.max(np.abs(lse.reshape(B, H, T) - l64)) < 1e-4
+    for got, want in zip((dq, dk, dv), causal_attention_grad_f64(q64, k64, v64, do64)):
+        assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
+
+
+# ------------------------------------------------------------------ KV decode
+def _kv_single(ctx, q_new, kh, vh, t_total, H, dh, max_len):
+    from aurora_amd.gpu import GpuBuffer, MhaKvCacheKernel
+
+    bq, bk, bv = (GpuBuffer.from_slice(ctx, x) for x in (q_new, kh, vh))
+    out = GpuBuffer.zeros(ctx, H * dh)
+    scratch = GpuBuffer.empty(ctx, MhaKvCacheKernel.scratch_len(H, max_len))
+    MhaKvCacheKernel.new(ctx).dispatch_into(ctx, bq, bk, bv, out, scratch, t_total, H, dh, max_len)
+    res = out.download()
+    for x in (bq, bk, bv, out, scratch):
+        x.free()
+    return res
+
+
+@pytest.mark.parametrize("t_total,H,dh", [(1, 2, 16), (5, 2, 16), (64, 2, 32), (80, 2, 16),
+                                          (129, 4, 64), (300, 1, 8), (513, 16, 64)])
+def test_mha_kv_step_matches_cpu(ctx, t_total, H, dh):
+    """tests/kv_cache.rs:346-386 covers t_total=80 > 64 (stride loops)."""
+    rng = np.random.default_rng(100 + t_total)
+    d, max_len = H * dh, max(t_total, 96)
+    q_new = _n(rng, d)
+    kh, vh = _n(rng, max_len * d), _n(rng, max_len * d)
+    got = _kv_single(ctx, q_new, kh, vh, t_total, H, dh, max_len)
+    want = oracle.kv_attend(q_new, kh, vh, t_total, H, dh)
+    assert max_rel_err(got, want) < TOL_REF
+    assert fro_rel(got, want) < TOL_ATTN
+
+
+def test_kv_step_equals_last_row_of_full_forward(ctx):
+    """The decode step's query against the cache equals the full causal
+    forward's last row (tests/kv_cache.rs:64-138 property, kernel level)."""
+    T, H, dh = 200, 4, 64
+    rng = np.random.default_rng(21)
+    d = H * dh
+    q, k, v = _n(rng, T * d), _n(rng, T * d), _n(rng, T * d)
+    out, _ = _fwd(ctx, q, k, v, 1, T, H, dh)
+    for t in (1, 64, 65, 128, 200):
+        got = _kv_single(ctx, q[(t - 1) * d:t * d], k, v, t, H, dh, T)
+        np.testing.assert_allclose(got, out.reshape(T, d)[t - 1], rtol=0, atol=2e-5)
+
+
+def test_kv_step_batched_ragged_lengths(ctx):
+    from aurora_amd.gpu import GpuBuffer, MhaKvCacheKernel
+
+    B, H, dh, max_len = 5, 4, 64, 300
+    rng = np.random.default_rng(31)
+    d = H * dh
+    lens = np.array([1, 64, 129, 300, 257], np.int32)
+    q_new = _n(rng, B * d)
+    kh, vh = _n(rng, B * max_len * d), _n(rng, B * max_len * d)
+    bq, bk, bv = (GpuBuffer.from_slice(ctx, x) for x in (q_new, kh, vh))
+    bt = GpuBuffer.from_slice(ctx, lens)
+    out = GpuBuffer.zeros(ctx, B * d)
+    scratch = GpuBuffer.empty(ctx, MhaKvCacheKernel.scratch_len(H, max_len, B))
+    MhaKvCacheKernel.new(ctx).dispatch_batched(ctx, bq, bk, bv, out, scratch, bt, int(lens.max()),
+                                               B, H, dh, max_len)
+    got = out.download().reshape(B, d)
+    for i in range(B):
+        want = oracle.kv_attend(q_new[i * d:(i + 1) * d], kh[i * max_len * d:(i + 1) * max_len * d],
+                                vh[i * max_len * d:(i + 1) * max_len * d], int(lens[i]), H, dh)
+        assert fro_rel(got[i], want) < TOL_ATTN, i

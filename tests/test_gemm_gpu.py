@@ -1,0 +1,207 @@
+"""GPU parity of the GEMM family (A@B, A@Bᵀ, dest += dYᵀ·X) through the C ABI.
+
+Mirrors tests/gpu_parity.rs:57-109 (gemm / gemm_transpose_b) and :469-508
+(outer_product_accum with a non-zero initial dest) at the reference's own
+tiny shapes against the CPU restatement, then the BASELINE config-1 sweep
+(M = 8192) against a float64 product with normalised gates (see parity.py).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests.parity import componentwise, fro_rel, max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL_GEMM = 1e-4  # <= 1e-4 per GEMM (normalised, vs float64)
+TOL_REF = 5e-3   # tests/gpu_parity.rs:81, pointwise vs the fp32 CPU oracle
+
+
+def _u(rng, n):
+    return rng.uniform(-1.0, 1.0, n).astype(np.float32)
+
+
+def _run(ctx, fn, a, b, c_len, *dims, c_init=None):
+    from aurora_amd.gpu import GpuBuffer
+
+    ab = GpuBuffer.from_slice(ctx, a)
+    bb = GpuBuffer.from_slice(ctx, b)
+    cb = GpuBuffer.from_slice(ctx, c_init) if c_init is not None else GpuBuffer.zeros(ctx, c_len)
+    fn(ctx, ab, bb, cb, *dims)
+    out = cb.download()
+    for x in (ab, bb, cb):
+        x.free()
+    return out
+
+
+def _nn(ctx, a, b, m, n, k):
+    from aurora_amd.gpu import GemmKernel
+
+    return _run(ctx, GemmKernel.new(ctx).dispatch_into, a, b, m * n, m, n, k)
+
+
+def _nt(ctx, a, b, m, n, k):
+    from aurora_amd.gpu import GemmTransposeBKernel
+
+    return _run(ctx, GemmTransposeBKernel.new(ctx).dispatch_into, a, b, m * n, m, n, k)
+
+
+def _outer(ctx, x, dy, dest, d_out, d_in, t):
+    from aurora_amd.gpu import OuterProductAccumKernel
+
+    return _run(ctx, OuterProductAccumKernel.new(ctx).dispatch_into, x, dy, d_out * d_in,
+                d_out, d_in, t, c_init=dest)
+
+
+def _gates(c, a64, b64, c0=None):
+    """Componentwise + Frobenius error of c against the float64 product."""
+    c64 = a64 @ b64
+    bound = np.abs(a64) @ np.abs(b64)
+    if c0 is not None:
+        c64 = c64 + c0
+        bound = bound + np.abs(c0)
+    c = c.reshape(c64.shape)
+    return componentwise(c, c64, bound), fro_rel(c, c64)
+
+
+@pytest.mark.parametrize("m,k,n", [(16, 16, 16), (33, 64, 17), (8, 128, 64), (64, 32, 96)])
+def test_gemm_matches_cpu(ctx, m, k, n):
+    """tests/gpu_parity.rs:57-82 shapes."""
+    rng = np.random.default_rng(1000 + m + k + n)
+    a, b = _u(rng, m * k), _u(rng, k * n)
+    got = _nn(ctx, a, b, m, n, k)
+    want = oracle.cpu_gemm(a, b, m, k, n)
+    assert max_rel_err(got, want) < TOL_REF
+    cw, fr = _gates(got, a.reshape(m, k).astype(np.float64), b.reshape(k, n).astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
+
+
+@pytest.mark.parametrize("m,k,n", [(16, 16, 16), (32, 48, 20), (8, 64, 64)])
+def test_gemm_transpose_b_matches_cpu(ctx, m, k, n):
+    """tests/gpu_parity.rs:84-109 shapes."""
+    rng = np.random.default_rng(2000 + m + k + n)
+    a, b = _u(rng, m * k), _u(rng, n * k)
+    got = _nt(ctx, a, b, m, n, k)
+    want = oracle.cpu_gemm_transpose_b(a, b, m, k, n)
+    assert max_rel_err(got, want) < TOL_REF
+    cw, fr = _gates(got, a.reshape(m, k).astype(np.float64), b.reshape(n, k).T.astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
+
+
+@pytest.mark.parametrize("d_out,d_in,t", [(16, 16, 8), (32, 64, 12), (8, 24, 16)])
+def test_outer_product_accum_matches_cpu(ctx, d_out, d_in, t):
+    """tests/gpu_parity.rs:469-508: accumulate into a NON-ZERO dest."""
+    rng = np.random.default_rng(3000 + d_out + d_in + t)
+    x, dy, dest = _u(rng, t * d_in), _u(rng, t * d_out), _u(rng, d_out * d_in)
+    got = _outer(ctx, x, dy, dest, d_out, d_in, t)
+    want = dest.copy()
+    oracle.outer_accum(x, dy, want, d_out, d_in, t)
+    assert max_rel_err(got, want) < TOL_REF
+    cw, fr = _gates(got, dy.reshape(t, d_out).T.astype(np.float64),
+                    x.reshape(t, d_in).astype(np.float64), dest.reshape(d_out, d_in))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (130, 33, 70), (257, 1000, 129), (3, 7, 5),
+                                   (128, 2048, 128), (64, 4096, 8)])
+def test_ragged_shapes_all_forms(ctx, m, k, n):
+    """Edge tiles, K tails, non-multiple-of-4 strides (scalar load path),
+    and split-K at long K with a small output."""
+    rng = np.random.default_rng(4000 + m * 7 + k * 3 + n)
+    a = _u(rng, m * k)
+    b_nn = _u(rng, k * n)
+    b_nt = _u(rng, n * k)
+    a64 = a.reshape(m, k).astype(np.float64)
+    cw, fr = _gates(_nn(ctx, a, b_nn, m, n, k), a64, b_nn.reshape(k, n).astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("nn", cw, fr)
+    cw, fr = _gates(_nt(ctx, a, b_nt, m, n, k), a64, b_nt.reshape(n, k).T.astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("nt", cw, fr)
+    # outer accum with d_out = m, d_in = n, t = k
+    x, dy, dest = _u(rng, k * n), _u(rng, k * m), _u(rng, m * n)
+    got = _outer(ctx, x, dy, dest, m, n, k)
+    cw, fr = _gates(got, dy.reshape(k, m).T.astype(np.float64), x.reshape(k, n).astype(np.float64),
+                    dest.reshape(m, n))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("outer", cw, fr)
+
+
+def test_k_zero_overwrites_and_accumulate_keeps(ctx):
+    from aurora_amd.gpu import GpuBuffer
+
+    c = GpuBuffer.from_slice(ctx, np.full(12, 7.0, np.float32))
+    a = GpuBuffer.zeros(ctx, 4)
+    ctx.call("aur_gemm_nn", a.ptr, a.ptr, c.ptr, 3, 4, 0)
+    assert np.all(c.download() == 0.0)
+    c.upload(np.full(12, 7.0, np.float32))
+    ctx.call("aur_outer_accum", a.ptr, a.ptr, c.ptr, 3, 4, 0)
+    assert np.all(c.download() == 7.0)
+
+
+def test_strided_gemm_ex_submatrix(ctx):
+    """aur_gemm_ex on a sub-block: lda/ldb/ldc larger than the logical width."""
+    from aurora_amd.gpu import GpuBuffer
+
+    rng = np.random.default_rng(5)
+    M, N, K, lda, ldb, ldc = 96, 80, 72, 100, 84, 92
+    A = _u(rng, M * lda)
+    B = _u(rng, N * ldb)  # B(k,n) = b[n*ldb + k]  (k-contiguous)
+    C0 = _u(rng, M * ldc)
+    ab, bb, cb = GpuBuffer.from_slice(ctx, A), GpuBuffer.from_slice(ctx, B), GpuBuffer.from_slice(ctx, C0)
+    ctx.call("aur_gemm_ex", 1, 1, ab.ptr, lda, bb.ptr, ldb, cb.ptr, ldc, M, N, K, 1)
+    got = cb.download().reshape(M, ldc)
+    a64 = A.reshape(M, lda)[:, :K].astype(np.float64)
+    b64 = B.reshape(N, ldb)[:, :K].T.astype(np.float64)
+    want = C0.reshape(M, ldc).astype(np.float64).copy()
+    want[:, :N] += a64 @ b64
+    assert np.array_equal(got[:, N:], C0.reshape(M, ldc)[:, N:])  # untouched padding
+    assert fro_rel(got[:, :N], want[:, :N]) < TOL_GEMM
+
+
+# ---- M = B·T = 8192 sweep ------------------------------
+SWEEP = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
+
+
+@pytest.mark.parametrize("k,n", SWEEP)
+def test_config1_sweep_nn_nt(ctx, k, n):
+    m = 8192
+    rng = np.random.default_rng(10_000 + k + n)
+    a = _u(rng, m * k)
+    b = _u(rng, k * n)
+    a64 = a.reshape(m, k).astype(np.float64)
+    b64 = b.reshape(k, n).astype(np.float64)
+    cw, fr = _gates(_nn(ctx, a, b, m, n, k), a64, b64)
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("nn", cw, fr)
+    bt = np.ascontiguousarray(b.reshape(k, n).T).ravel()  # B as [n, k]
+    cw, fr = _gates(_nt(ctx, a, bt, m, n, k), a64, b64)
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("nt", cw, fr)
+
+
+def test_config1_tied_head(ctx):
+    m, k, n = 8192, 512, 8192
+    rng = np.random.default_rng(10_001)
+    h, w_tok = _u(rng, m * k), _u(rng, n * k)
+    got = _nt(ctx, h, w_tok, m, n, k)
+    cw, fr = _gates(got, h.reshape(m, k).astype(np.float64), w_tok.reshape(n, k).T.astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
+
+
+def test_config1_weight_grad_accumulate(ctx):
+    """X[8192,512], dY[8192,2048] summed into an existing dest[2048,512]."""
+    t, d_in, d_out = 8192, 512, 2048
+    rng = np.random.default_rng(10_002)
+    x, dy, dest = _u(rng, t * d_in), _u(rng, t * d_out), _u(rng, d_out * d_in)
+    got = _outer(ctx, x, dy, dest, d_out, d_in, t)
+    cw, fr = _gates(got, dy.reshape(t, d_out).T.astype(np.float64),
+                    x.reshape(t, d_in).astype(np.float64), dest.reshape(d_out, d_in))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
+    # Deterministic: the split-K reduction has a fixed order.
+    again = _outer(ctx, x, dy, dest, d_out, d_in, t)
+    assert np.array_equal(got, again)
+
+
+def test_nt_equals_nn_on_materialised_transpose(ctx):
+    m, k, n = 300, 257, 190
+    rng = np.random.default_rng(7)
+    a, b = _u(rng, m * k), _u(rng, n * k)
+    nt = _nt(ctx, a, b, m, n, k)
+    nn = _nn(ctx, a, np.ascontiguousarray(b.reshape(n, k).T).ravel(), m, n, k)
+    assert fro_rel(nt, nn) < 1e-6
