@@ -49,6 +49,29 @@ SIGNATURES: dict[str, tuple] = {
     "aur_mha_kv_step": (_i32, [_c_ctx, _f, _f, _f, _f, _f, _u32, _u32, _u32, _u32]),
     "aur_mha_kv_step_batched": (_i32, [_c_ctx, _f, _f, _f, _f, _f, _f, _u32,
                                        _u32, _u32, _u32, _u32]),
+    "aur_model_create": (_i32, [_c_ctx, C.c_void_p, _u32, C.POINTER(C.c_void_p)]),
+    "aur_model_destroy": (_i32, [C.c_void_p]),
+    "aur_model_tensor": (_i32, [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32,
+                                C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
+    "aur_model_zero_grad": (_i32, [C.c_void_p]),
+    "aur_model_train_step_batch": (_i32, [C.c_void_p, C.c_void_p, C.c_void_p, _u32, _u32,
+                                          C.POINTER(C.c_float)]),
+    "aur_model_forward": (_i32, [C.c_void_p, C.c_void_p, _u32, _u32, C.c_void_p]),
+    "aur_model_clip_grads": (_i32, [C.c_void_p, C.c_float, C.POINTER(C.c_float)]),
+    "aur_model_step_adamw": (_i32, [C.c_void_p, C.c_float, C.c_float, C.c_float, C.c_float,
+                                    C.c_float]),
+    "aur_model_clip_step_adamw": (_i32, [C.c_void_p, C.c_float, C.c_float, C.c_float, C.c_float,
+                                         C.c_float, C.c_float, C.POINTER(C.c_float)]),
+    "aur_kv_cache_create": (_i32, [C.c_void_p, _u32, _u32, C.POINTER(C.c_void_p)]),
+    "aur_kv_cache_reset": (_i32, [C.c_void_p]),
+    "aur_kv_cache_destroy": (_i32, [C.c_void_p]),
+    "aur_kv_cache_len": (_i32, [C.c_void_p, C.POINTER(_u32)]),
+    "aur_kv_cache_history": (_i32, [C.c_void_p, _u32, C.POINTER(C.c_void_p),
+                                    C.POINTER(C.c_void_p)]),
+    "aur_model_prefill_kv": (_i32, [C.c_void_p, C.c_void_p, C.c_void_p, _u32, _u32, C.c_void_p]),
+    "aur_model_generate_step": (_i32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_void_p]),
+    "aur_model_generate_greedy": (_i32, [C.c_void_p, C.c_void_p, _u32, C.c_void_p]),
 }
 
 

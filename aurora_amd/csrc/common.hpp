@@ -29,6 +29,30 @@ int set_error(aur_ctx* ctx, int code, const char* fmt, ...);
 // Makes `ctx` own at least `bytes` of workspace; returns 0 or an error code.
 int ensure_workspace(aur_ctx* ctx, size_t bytes);
 
+// Output forms fused into the GEMM store; v = (A·B)(row, col), and R, X, C2
+// are addressed with C's leading dimension.
+enum EpiMode : int {
+  EPI_STORE = 0,     // C = v
+  EPI_ACCUM = 1,     // C = C + v
+  EPI_RESID = 2,     // C = R + v            (residual add)
+  EPI_GELU = 3,      // C = v, C2 = gelu(v)  (FFN up-projection keeps both)
+  EPI_GELU_BWD = 4,  // C = v · gelu'(X)     (FFN backward through the activation)
+};
+
+struct Epilogue {
+  int mode = EPI_STORE;
+  const float* R = nullptr;
+  const float* X = nullptr;
+  float* C2 = nullptr;
+};
+
+// C = epilogue(op(A)·op(B)).  a_kcontig: A(m,k) = A[m*lda+k], else A[k*lda+m];
+// b_kcontig: B(k,n) = B[n*ldb+k], else B[k*ldb+n].  Enqueued on ctx's stream.
+int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
+         int ldb, float* C, int ldc, int M, int N, int K, const Epilogue& epi);
+int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
+         int ldb, float* C, int ldc, int M, int N, int K, bool accumulate);
+
 }  // namespace aur
 
 #define AUR_CHECK_CTX(ctx)                                   \

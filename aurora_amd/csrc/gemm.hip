@@ -37,9 +37,40 @@ struct GemmArgs {
   int M, N, K;
   int lda, ldb, ldc;
   int k_chunk;  // K range per blockIdx.z (multiple of BK)
-  int mode;     // 0: C = AB, 1: C += AB, 2: P[z] = partial AB
+  int split;    // 1: write partial tiles to P[z] (epilogue runs in splitk_reduce)
   int tiles_m, tiles_n;
+  aur::Epilogue epi;
 };
+
+// Fused epilogue on one output element v = (A·B)(row, col), stored at C[i]
+// with i = row*ldc + col (R, X, C2 share C's layout).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // src/linalg.rs:72-77: 0.5·x·(1 + tanh(√(2/π)·(x + 0.044715·x³)))
+  const float k = 0.7978845608028654f;
+  return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+}
+
+__device__ __forceinline__ float gelu_tanh_grad(float x) {
+  // src/linalg.rs:81-87
+  const float k = 0.7978845608028654f;
+  const float th = tanhf(k * (x + 0.044715f * x * x * x));
+  const float sech2 = 1.0f - th * th;
+  return 0.5f * (1.0f + th) + 0.5f * x * sech2 * (k * (1.0f + 3.0f * 0.044715f * x * x));
+}
+
+__device__ __forceinline__ void apply_epilogue(const aur::Epilogue& e, float* __restrict__ C, size_t i,
+                                               float v) {
+  switch (e.mode) {
+    case aur::EPI_ACCUM: C[i] = C[i] + v; break;
+    case aur::EPI_RESID: C[i] = e.R[i] + v; break;
+    case aur::EPI_GELU:
+      C[i] = v;
+      e.C2[i] = gelu_tanh(v);
+      break;
+    case aur::EPI_GELU_BWD: C[i] = v * gelu_tanh_grad(e.X[i]); break;
+    default: C[i] = v; break;
+  }
+}
 
 template <int BM, int BN, int BK, bool AK, bool BKC>
 struct Smem {
@@ -206,15 +237,6 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
   }
 
   // Epilogue: lane holds D[4·g16 + e][l16] of each 16×16 tile.
-  float* out;
-  int ldo;
-  if (g.mode == 2) {
-    out = g.P + (size_t)blockIdx.z * g.M * g.N;
-    ldo = g.N;
-  } else {
-    out = g.C;
-    ldo = g.ldc;
-  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -225,29 +247,28 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
       for (int e = 0; e < 4; ++e) {
         const int row = m0 + wm * WM + i * 16 + 4 * g16 + e;
         if (row < g.M) {
-          float* p = out + (size_t)row * ldo + col;
-          if (g.mode == 1)
-            *p += acc[i][j][e];
+          if (g.split)
+            g.P[((size_t)blockIdx.z * g.M + row) * g.N + col] = acc[i][j][e];
           else
-            *p = acc[i][j][e];
+            apply_epilogue(g.epi, g.C, (size_t)row * g.ldc + col, acc[i][j][e]);
         }
       }
     }
   }
 }
 
-// C(m,n) (+)= Σ_{z=0..splits-1} P[z][m][n], summed in increasing z.
+// v(m,n) = Σ_{z=0..splits-1} P[z][m][n] summed in increasing z, then the
+// fused epilogue writes C (and C2).
 __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ P, float* __restrict__ C,
                                                       int M, int N, int ldc, int splits,
-                                                      int accumulate) {
+                                                      aur::Epilogue epi) {
   const size_t total = (size_t)M * N;
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    float s = P[i];
-    for (int z = 1; z < splits; ++z) s += P[(size_t)z * total + i];
+    float s = 0.f;  // splits == 0 (K == 0): the epilogue of an empty product
+    for (int z = 0; z < splits; ++z) s += P[(size_t)z * total + i];
     const size_t row = i / N, col = i % N;
-    float* c = C + row * ldc + col;
-    *c = accumulate ? *c + s : s;
+    apply_epilogue(epi, C, row * ldc + col, s);
   }
 }
 
@@ -323,17 +344,22 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 namespace aur {
 
-// C (+)= op(A)·op(B) on ctx's stream.  See aur_gemm_ex for operand meaning.
+// C = epilogue(op(A)·op(B)) on ctx's stream.  See aur_gemm_ex for operand
+// meaning and Epilogue (common.hpp) for the fused output forms.
 int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
-         int ldb, float* C, int ldc, int M, int N, int K, bool accumulate) {
+         int ldb, float* C, int ldc, int M, int N, int K, const Epilogue& epi) {
   if (M < 0 || N < 0 || K < 0) return set_error(ctx, AUR_EINVAL, "gemm: negative dims");
   if (M == 0 || N == 0) return 0;
   if (!C || (K > 0 && (!A || !B))) return set_error(ctx, AUR_EINVAL, "gemm: null pointer");
+  if ((epi.mode == EPI_RESID && !epi.R) || (epi.mode == EPI_GELU && !epi.C2) ||
+      (epi.mode == EPI_GELU_BWD && !epi.X))
+    return set_error(ctx, AUR_EINVAL, "gemm: epilogue operand missing");
   if (K == 0) {
-    if (!accumulate) {
-      for (int r = 0; r < M; ++r)
-        AUR_HIP(ctx, hipMemsetAsync(C + (size_t)r * ldc, 0, sizeof(float) * N, ctx->stream));
-    }
+    const size_t total = (size_t)M * N;
+    int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, nullptr, C, M, N, ldc,
+                       0, epi);
+    AUR_LAUNCH_CHECK(ctx, "splitk_reduce(K=0)");
     return 0;
   }
   // The A / B "row" extents (the contiguous index of a k-strided operand).
@@ -356,14 +382,13 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
   a.tiles_m = (M + p.bm - 1) / p.bm;
   a.tiles_n = (N + p.bn - 1) / p.bn;
   a.k_chunk = p.k_chunk;
+  a.epi = epi;
   if (p.splits > 1) {
     const size_t need = (size_t)p.splits * M * N * sizeof(float);
     int rc = ensure_workspace(ctx, need);
     if (rc) return rc;
     a.P = static_cast<float*>(ctx->ws);
-    a.mode = 2;
-  } else {
-    a.mode = accumulate ? 1 : 0;
+    a.split = 1;
   }
   if (a_kcontig && b_kcontig)
     launch_layout<true, true>(a, p, vec, ctx->stream);
@@ -378,10 +403,17 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
     const size_t total = (size_t)M * N;
     int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
     hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, a.P, C, M, N, ldc,
-                       p.splits, accumulate ? 1 : 0);
+                       p.splits, epi);
     AUR_LAUNCH_CHECK(ctx, "splitk_reduce");
   }
   return 0;
+}
+
+int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
+         int ldb, float* C, int ldc, int M, int N, int K, bool accumulate) {
+  Epilogue e;
+  e.mode = accumulate ? EPI_ACCUM : EPI_STORE;
+  return gemm(ctx, a_kcontig, b_kcontig, A, lda, B, ldb, C, ldc, M, N, K, e);
 }
 
 }  // namespace aur

@@ -14,6 +14,7 @@
 //     a second kernel merges the chunks of a (sequence, head) in increasing
 //     chunk order — a fixed order, so the result is deterministic.
 #include "common.hpp"
+#include "step_ops.hpp"
 
 namespace {
 
@@ -33,7 +34,8 @@ struct KvArgs {
   float* ws;            // [B, H, nch, PART]
   const int32_t* t_dev; // per-sequence lengths (device) or null
   int t_scalar;         // length when t_dev is null
-  int ld;               // row stride (= n_head * d_head)
+  int ld;               // row stride of the history and out (= n_head * d_head)
+  int ld_q;             // row stride of q (d, or 3d inside a fused qkv row)
   int max_len;
   int H;
   int nch;
@@ -59,7 +61,7 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
     return;
   }
   const size_t hist = (size_t)b * a.max_len;
-  floatx4 qv = *reinterpret_cast<const floatx4*>(a.q + (size_t)b * a.ld + h * DH + 4 * part);
+  floatx4 qv = *reinterpret_cast<const floatx4*>(a.q + (size_t)b * a.ld_q + h * DH + 4 * part);
   qv *= a.scale * LOG2E;
 
   // Scores of this wave's keys, KPS per step (one per LPK-lane group).
@@ -190,7 +192,7 @@ int aur_mha_kv_step(aur_ctx* ctx, const float* q_new, const float* k_history, co
   KvArgs a{};
   a.q = q_new; a.kh = k_history; a.vh = v_history; a.out = out; a.ws = scratch;
   a.t_dev = nullptr; a.t_scalar = (int)t_total;
-  a.ld = (int)(n_head * d_head); a.max_len = (int)max_len; a.H = (int)n_head;
+  a.ld = (int)(n_head * d_head); a.ld_q = a.ld; a.max_len = (int)max_len; a.H = (int)n_head;
   a.scale = 1.0f / sqrtf((float)d_head);
   return launch(ctx, a, 1, (int)t_total, (int)d_head);
 }
@@ -200,19 +202,30 @@ int aur_mha_kv_step_batched(aur_ctx* ctx, const float* q_new, const float* k_his
                             uint32_t t_max, uint32_t b, uint32_t n_head, uint32_t d_head,
                             uint32_t max_len) {
   AUR_CHECK_CTX(ctx);
-  if (!dh_ok(d_head))
-    return aur::set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%u, supports 8/16/32/64", d_head);
-  if (b == 0 || n_head == 0 || t_max == 0 || t_max > max_len)
-    return aur::set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: b=%u t_max=%u max_len=%u", b, t_max,
-                          max_len);
-  if (!q_new || !k_history || !v_history || !out || !scratch || !t_total)
-    return aur::set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: null pointer");
-  KvArgs a{};
-  a.q = q_new; a.kh = k_history; a.vh = v_history; a.out = out; a.ws = scratch;
-  a.t_dev = t_total; a.t_scalar = 0;
-  a.ld = (int)(n_head * d_head); a.max_len = (int)max_len; a.H = (int)n_head;
-  a.scale = 1.0f / sqrtf((float)d_head);
-  return launch(ctx, a, (int)b, (int)t_max, (int)d_head);
+  return aur::mha_kv_batched(ctx, q_new, (int)(n_head * d_head), k_history, v_history, out, scratch,
+                             t_total, (int)t_max, (int)b, (int)n_head, (int)d_head, (int)max_len);
 }
 
 }  // extern "C"
+
+namespace aur {
+
+int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_history,
+                   const float* v_history, float* out, float* scratch, const int32_t* t_total, int t_max,
+                   int b, int n_head, int d_head, int max_len) {
+  if (!dh_ok((uint32_t)d_head))
+    return set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%d, supports 8/16/32/64", d_head);
+  if (b <= 0 || n_head <= 0 || t_max <= 0 || t_max > max_len || ld_q < n_head * d_head || (ld_q & 3))
+    return set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: b=%d t_max=%d max_len=%d ld_q=%d", b, t_max,
+                     max_len, ld_q);
+  if (!q || !k_history || !v_history || !out || !scratch || !t_total)
+    return set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: null pointer");
+  KvArgs a{};
+  a.q = q; a.kh = k_history; a.vh = v_history; a.out = out; a.ws = scratch;
+  a.t_dev = t_total; a.t_scalar = 0;
+  a.ld = n_head * d_head; a.ld_q = ld_q; a.max_len = max_len; a.H = n_head;
+  a.scale = 1.0f / sqrtf((float)d_head);
+  return launch(ctx, a, b, t_max, d_head);
+}
+
+}  // namespace aur

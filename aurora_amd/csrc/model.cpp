@@ -1,0 +1,698 @@
+// DecoderTransformerGpu / KvCacheGpu: the caller of the GEMM + attention hot
+// path, at M = B·T rows, plus its C ABI (aur_model_*, aur_kv_cache_*).
+//
+// Reference: src/gpu/transformer.rs (encode_forward :1347, train step
+// :1535-1716, block_backward :1825-2005, AdamW :2008, prefill / decode
+// :2374-2640) and the CPU model it must agree with, src/transformer/
+// {model,block,attention,ffn,embedding,kv_cache}.rs.
+//
+// One step enqueues, per layer, 4 forward GEMMs (fused QKV, W_o with the
+// residual add in its epilogue, fc with GELU in its epilogue, proj with the
+// residual add), 4 dX GEMMs (GELU' fused into the proj-dX epilogue) and
+// 4 weight-gradient accumulates, plus the flash attention forward / 3-pass
+// backward and the row kernels of step_ops.hip.  Everything stays on the
+// device; the host reads back only the per-row NLL (one small copy per step).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+#include <vector>
+
+#include "aurora.hpp"
+#include "common.hpp"
+#include "step_ops.hpp"
+
+namespace aurora {
+
+namespace {
+
+constexpr float kLnEps = 1e-5f;  // LayerNorm::new (src/attention.rs:44)
+
+// Bump allocator over one device allocation (256-byte aligned slices).
+struct Carver {
+  char* base;
+  size_t off = 0;
+  template <class T>
+  T* take(size_t n) {
+    off = (off + 255) & ~size_t(255);
+    T* p = reinterpret_cast<T*>(base + off);
+    off += n * sizeof(T);
+    return p;
+  }
+};
+
+inline void ck(aur_ctx* ctx, int rc, const char* what) { check(ctx, rc, what); }
+
+}  // namespace
+
+struct DecoderTransformerGpu::Layer {
+  // parameters (views into the flat parameter buffer) and their gradients
+  float *ln1_g, *ln1_b, *w_qkv, *w_o, *ln2_g, *ln2_b, *w_fc, *w_proj;
+  float *g_ln1_g, *g_ln1_b, *g_w_qkv, *g_w_o, *g_ln2_g, *g_ln2_b, *g_w_fc, *g_w_proj;
+  // saved activations of the last forward
+  float *ln1, *mean1, *rstd1, *qkv, *attn, *lse, *xmid, *ln2, *mean2, *rstd2, *hpre, *hpost;
+};
+
+struct DecoderTransformerGpu::Acts {
+  size_t rows;
+  std::vector<float*> xs;  // residual stream: xs[l] = input of layer l, xs[L] = final
+  float *lnf, *meanf, *rstdf, *logits, *nll;
+  float *dx_a, *dx_b, *dln, *dh, *dqkv, *dattn;
+  float *ln_ws, *attn_ws, *norm_part, *stats, *last;
+  uint32_t *tok, *tgt, *csr_tok;
+  int32_t *csr_off, *csr_idx;
+  float *w_tok, *w_pos, *lnf_g, *lnf_b, *g_w_tok, *g_w_pos, *g_lnf_g, *g_lnf_b;
+  std::vector<float> nll_host;
+};
+
+DecoderTransformerGpu::DecoderTransformerGpu(aur_ctx* ctx, const TransformerConfig& cfg,
+                                             uint32_t max_batch)
+    : ctx_(ctx), cfg_(cfg), max_batch_(max_batch) {
+  const size_t V = cfg.vocab, d = cfg.d_model, L = cfg.n_layer, F = cfg.d_ff, Tm = cfg.seq_len_max;
+  if (!ctx || V == 0 || d == 0 || L == 0 || F == 0 || Tm == 0 || max_batch == 0 || cfg.n_head == 0 ||
+      d % cfg.n_head != 0)
+    throw Error("DecoderTransformerGpu: invalid config", AUR_EINVAL);
+  const uint32_t dh = cfg.d_model / cfg.n_head;
+  if (!(dh == 8 || dh == 16 || dh == 32 || dh == 64))
+    throw Error("DecoderTransformerGpu: d_head must be 8, 16, 32 or 64", AUR_ELIMIT);
+  if (d % 4 != 0 || F % 4 != 0 || V % 4 != 0)
+    throw Error("DecoderTransformerGpu: vocab, d_model, d_ff must be multiples of 4", AUR_EINVAL);
+  // Flat parameter layout: weight-decayed tensors first (w_tok, then per
+  // layer w_qkv = [w_q; w_k; w_v], w_o, w_fc, w_proj), then the undecayed
+  // ones (w_pos, per layer ln1_g, ln1_b, ln2_g, ln2_b, then lnf_g, lnf_b).
+  n_decay_ = V * d + L * (3 * d * d + d * d + F * d + d * F);
+  n_params_ = n_decay_ + Tm * d + L * 4 * d + 2 * d;
+  ck(ctx_, aur_malloc(ctx_, 4 * n_params_ * sizeof(float) + 4096, &state_mem_), "alloc params");
+  params_ = static_cast<float*>(state_mem_);
+  grads_ = params_ + n_params_;
+  m1_ = grads_ + n_params_;
+  m2_ = m1_ + n_params_;
+  ck(ctx_, aur_memset0(ctx_, state_mem_, 4 * n_params_ * sizeof(float)), "zero state");
+
+  layers_ = new std::vector<Layer>(L);
+  acts_ = new Acts();
+  auto& A = *acts_;
+  size_t off = 0;
+  auto pv = [&](size_t n) {
+    size_t o = off;
+    off += n;
+    return o;
+  };
+  const size_t o_wtok = pv(V * d);
+  std::vector<size_t> o_qkv(L), o_wo(L), o_fc(L), o_proj(L);
+  for (size_t l = 0; l < L; ++l) {
+    o_qkv[l] = pv(3 * d * d);
+    o_wo[l] = pv(d * d);
+    o_fc[l] = pv(F * d);
+    o_proj[l] = pv(d * F);
+  }
+  const size_t o_wpos = pv(Tm * d);
+  std::vector<size_t> o_ln(L);
+  for (size_t l = 0; l < L; ++l) o_ln[l] = pv(4 * d);
+  const size_t o_lnf = pv(2 * d);
+  A.w_tok = params_ + o_wtok;
+  A.g_w_tok = grads_ + o_wtok;
+  A.w_pos = params_ + o_wpos;
+  A.g_w_pos = grads_ + o_wpos;
+  A.lnf_g = params_ + o_lnf;
+  A.lnf_b = A.lnf_g + d;
+  A.g_lnf_g = grads_ + o_lnf;
+  A.g_lnf_b = A.g_lnf_g + d;
+  for (size_t l = 0; l < L; ++l) {
+    Layer& Y = (*layers_)[l];
+    Y.w_qkv = params_ + o_qkv[l];
+    Y.w_o = params_ + o_wo[l];
+    Y.w_fc = params_ + o_fc[l];
+    Y.w_proj = params_ + o_proj[l];
+    Y.ln1_g = params_ + o_ln[l];
+    Y.ln1_b = Y.ln1_g + d;
+    Y.ln2_g = Y.ln1_g + 2 * d;
+    Y.ln2_b = Y.ln1_g + 3 * d;
+    Y.g_w_qkv = grads_ + o_qkv[l];
+    Y.g_w_o = grads_ + o_wo[l];
+    Y.g_w_fc = grads_ + o_fc[l];
+    Y.g_w_proj = grads_ + o_proj[l];
+    Y.g_ln1_g = grads_ + o_ln[l];
+    Y.g_ln1_b = Y.g_ln1_g + d;
+    Y.g_ln2_g = Y.g_ln1_g + 2 * d;
+    Y.g_ln2_b = Y.g_ln1_g + 3 * d;
+  }
+
+  // Activation arena for max_batch × seq_len_max rows.
+  const size_t M = (size_t)max_batch * Tm;
+  const size_t H = cfg.n_head;
+  A.rows = M;
+  const size_t per_layer = M * d /*ln1*/ + 2 * M /*stats*/ + 3 * M * d /*qkv*/ + M * d /*attn*/ +
+                           H * M /*lse*/ + M * d /*xmid*/ + M * d /*ln2*/ + 2 * M + 2 * M * F;
+  const size_t lnws = aur::layer_norm_backward_ws_floats((int)M, (int)d);
+  const size_t floats = L * per_layer + (L + 1) * M * d + M * d + 2 * M + M * V + M +
+                        4 * M * d + M * F + 3 * M * d + lnws + H * M + aur::grad_norm_ws_floats() + 16 +
+                        (size_t)max_batch * d;
+  const size_t ints = 3 * M + 2 * M + 2;
+  const size_t bytes = floats * 4 + ints * 4 + 64 * 256 + 4096 * (L + 8);
+  ck(ctx_, aur_malloc(ctx_, bytes, &act_mem_), "alloc activations");
+  Carver cv{static_cast<char*>(act_mem_)};
+  A.xs.resize(L + 1);
+  for (size_t l = 0; l <= L; ++l) A.xs[l] = cv.take<float>(M * d);
+  for (size_t l = 0; l < L; ++l) {
+    Layer& Y = (*layers_)[l];
+    Y.ln1 = cv.take<float>(M * d);
+    Y.mean1 = cv.take<float>(M);
+    Y.rstd1 = cv.take<float>(M);
+    Y.qkv = cv.take<float>(3 * M * d);
+    Y.attn = cv.take<float>(M * d);
+    Y.lse = cv.take<float>(H * M);
+    Y.xmid = cv.take<float>(M * d);
+    Y.ln2 = cv.take<float>(M * d);
+    Y.mean2 = cv.take<float>(M);
+    Y.rstd2 = cv.take<float>(M);
+    Y.hpre = cv.take<float>(M * F);
+    Y.hpost = cv.take<float>(M * F);
+  }
+  A.lnf = cv.take<float>(M * d);
+  A.meanf = cv.take<float>(M);
+  A.rstdf = cv.take<float>(M);
+  A.logits = cv.take<float>(M * V);
+  A.nll = cv.take<float>(M);
+  A.dx_a = cv.take<float>(M * d);
+  A.dx_b = cv.take<float>(M * d);
+  A.dln = cv.take<float>(M * d);
+  A.dattn = cv.take<float>(M * d);
+  A.dh = cv.take<float>(M * F);
+  A.dqkv = cv.take<float>(3 * M * d);
+  A.ln_ws = cv.take<float>(lnws);
+  A.attn_ws = cv.take<float>(H * M);
+  A.norm_part = cv.take<float>(aur::grad_norm_ws_floats());
+  A.stats = cv.take<float>(16);
+  A.last = cv.take<float>((size_t)max_batch * d);
+  A.tok = cv.take<uint32_t>(M);
+  A.tgt = cv.take<uint32_t>(M);
+  A.csr_tok = cv.take<uint32_t>(M);
+  A.csr_off = cv.take<int32_t>(M + 1);
+  A.csr_idx = cv.take<int32_t>(M);
+  if (cv.off > bytes) throw Error("DecoderTransformerGpu: arena overflow", AUR_ENOMEM);
+}
+
+DecoderTransformerGpu::~DecoderTransformerGpu() {
+  if (ctx_) {
+    aur_sync(ctx_);
+    aur_free(ctx_, act_mem_);
+    aur_free(ctx_, state_mem_);
+  }
+  delete layers_;
+  delete acts_;
+}
+
+float* DecoderTransformerGpu::tensor(const std::string& name, int layer, bool grad, size_t* n) const {
+  const size_t V = cfg_.vocab, d = cfg_.d_model, F = cfg_.d_ff, Tm = cfg_.seq_len_max;
+  const auto& A = *acts_;
+  auto ret = [&](float* p, size_t len) {
+    if (n) *n = len;
+    return p;
+  };
+  if (name == "params") return ret(grad ? grads_ : params_, n_params_);
+  if (name == "grads") return ret(grads_, n_params_);
+  if (name == "w_tok") return ret(grad ? A.g_w_tok : A.w_tok, V * d);
+  if (name == "w_pos") return ret(grad ? A.g_w_pos : A.w_pos, Tm * d);
+  if (name == "lnf_g") return ret(grad ? A.g_lnf_g : A.lnf_g, d);
+  if (name == "lnf_b") return ret(grad ? A.g_lnf_b : A.lnf_b, d);
+  if (layer < 0 || layer >= (int)cfg_.n_layer) return nullptr;
+  const Layer& Y = (*layers_)[layer];
+  if (name == "ln1_g") return ret(grad ? Y.g_ln1_g : Y.ln1_g, d);
+  if (name == "ln1_b") return ret(grad ? Y.g_ln1_b : Y.ln1_b, d);
+  if (name == "ln2_g") return ret(grad ? Y.g_ln2_g : Y.ln2_g, d);
+  if (name == "ln2_b") return ret(grad ? Y.g_ln2_b : Y.ln2_b, d);
+  if (name == "w_qkv") return ret(grad ? Y.g_w_qkv : Y.w_qkv, 3 * d * d);
+  if (name == "w_q") return ret(grad ? Y.g_w_qkv : Y.w_qkv, d * d);
+  if (name == "w_k") return ret((grad ? Y.g_w_qkv : Y.w_qkv) + d * d, d * d);
+  if (name == "w_v") return ret((grad ? Y.g_w_qkv : Y.w_qkv) + 2 * d * d, d * d);
+  if (name == "w_o") return ret(grad ? Y.g_w_o : Y.w_o, d * d);
+  if (name == "w_fc") return ret(grad ? Y.g_w_fc : Y.w_fc, F * d);
+  if (name == "w_proj") return ret(grad ? Y.g_w_proj : Y.w_proj, d * F);
+  return nullptr;
+}
+
+void DecoderTransformerGpu::zero_grad() {
+  ck(ctx_, aur_memset0(ctx_, grads_, n_params_ * sizeof(float)), "zero_grad");
+}
+
+void DecoderTransformerGpu::upload_tokens(const uint32_t* tokens, const uint32_t* targets, uint32_t b,
+                                          uint32_t t) {
+  const size_t M = (size_t)b * t;
+  for (size_t i = 0; i < M; ++i)
+    if (tokens[i] >= cfg_.vocab) throw Error("token id out of vocab", AUR_EINVAL);
+  ck(ctx_, aur_h2d(ctx_, acts_->tok, tokens, M * 4), "upload tokens");
+  if (targets) {
+    for (size_t i = 0; i < M; ++i)
+      if (targets[i] >= cfg_.vocab) throw Error("target id out of vocab", AUR_EINVAL);
+    ck(ctx_, aur_h2d(ctx_, acts_->tgt, targets, M * 4), "upload targets");
+  }
+}
+
+void DecoderTransformerGpu::encode_forward(uint32_t b, uint32_t t, KvCacheGpu* cache, bool head_all_rows) {
+  auto& A = *acts_;
+  const int M = (int)(b * t), d = (int)cfg_.d_model, F = (int)cfg_.d_ff, V = (int)cfg_.vocab;
+  const int H = (int)cfg_.n_head, dh = d / H;
+  ck(ctx_, aur::embed_forward(ctx_, A.w_tok, A.w_pos, A.tok, nullptr, (int)t, A.xs[0], M, d), "embed");
+  for (uint32_t l = 0; l < cfg_.n_layer; ++l) {
+    Layer& Y = (*layers_)[l];
+    ck(ctx_, aur::layer_norm_forward(ctx_, A.xs[l], Y.ln1_g, Y.ln1_b, Y.ln1, Y.mean1, Y.rstd1, M, d, kLnEps),
+       "ln1");
+    // qkv[M, 3d] = ln1 · [w_q; w_k; w_v]ᵀ  (attention.rs:219 linear_forward ×3)
+    ck(ctx_, aur::gemm(ctx_, true, true, Y.ln1, d, Y.w_qkv, d, Y.qkv, 3 * d, M, 3 * d, d, false), "qkv");
+    if (cache)
+      ck(ctx_, aur::kv_store(ctx_, Y.qkv, d, cache->k_history(l), cache->v_history(l), (int)cache->max_len,
+                             nullptr, M, (int)t),
+         "kv_store");
+    ck(ctx_, aur_mha_fwd_ex(ctx_, Y.qkv, Y.qkv + d, Y.qkv + 2 * d, 3 * d, Y.attn, d, Y.lse, b, t, H, dh),
+       "mha_fwd");
+    // xmid = x + attn · w_oᵀ  (block.rs:167-172)
+    aur::Epilogue resid;
+    resid.mode = aur::EPI_RESID;
+    resid.R = A.xs[l];
+    ck(ctx_, aur::gemm(ctx_, true, true, Y.attn, d, Y.w_o, d, Y.xmid, d, M, d, d, resid), "w_o");
+    ck(ctx_, aur::layer_norm_forward(ctx_, Y.xmid, Y.ln2_g, Y.ln2_b, Y.ln2, Y.mean2, Y.rstd2, M, d, kLnEps),
+       "ln2");
+    // hpre = ln2 · w_fcᵀ, hpost = gelu(hpre)  (ffn.rs:91-105)
+    aur::Epilogue ge;
+    ge.mode = aur::EPI_GELU;
+    ge.C2 = Y.hpost;
+    ck(ctx_, aur::gemm(ctx_, true, true, Y.ln2, d, Y.w_fc, d, Y.hpre, F, M, F, d, ge), "w_fc");
+    // z = xmid + hpost · w_projᵀ
+    aur::Epilogue r2;
+    r2.mode = aur::EPI_RESID;
+    r2.R = Y.xmid;
+    ck(ctx_, aur::gemm(ctx_, true, true, Y.hpost, F, Y.w_proj, F, A.xs[l + 1], d, M, d, F, r2), "w_proj");
+  }
+  const float* xf = A.xs[cfg_.n_layer];
+  ck(ctx_, aur::layer_norm_forward(ctx_, xf, A.lnf_g, A.lnf_b, A.lnf, A.meanf, A.rstdf, M, d, kLnEps), "lnf");
+  if (head_all_rows) {
+    // tied head: logits = lnf · w_tokᵀ  (embedding.rs:152-169)
+    ck(ctx_, aur::gemm(ctx_, true, true, A.lnf, d, A.w_tok, d, A.logits, V, M, V, d, false), "head");
+  } else {
+    // last position of each sequence only
+    ck(ctx_, aur::gather_rows(ctx_, A.lnf, d, (int)t, (int)t - 1, A.last, (int)b, d), "gather last");
+    ck(ctx_, aur::gemm(ctx_, true, true, A.last, d, A.w_tok, d, A.logits, V, (int)b, V, d, false), "head");
+  }
+  (void)F;
+}
+
+void DecoderTransformerGpu::encode_backward(uint32_t b, uint32_t t) {
+  auto& A = *acts_;
+  const int M = (int)(b * t), d = (int)cfg_.d_model, F = (int)cfg_.d_ff, V = (int)cfg_.vocab;
+  const int H = (int)cfg_.n_head, dh = d / H;
+  float* dlog = A.logits;  // softmax-CE wrote d_logits in place
+  // d_h_final = d_logits · w_tok ; g_w_tok += d_logitsᵀ · h_final  (embedding.rs:175-206)
+  ck(ctx_, aur::gemm(ctx_, true, false, dlog, V, A.w_tok, d, A.dln, d, M, d, V, false), "head dX");
+  ck(ctx_, aur::gemm(ctx_, false, false, dlog, V, A.lnf, d, A.g_w_tok, d, V, d, M, true), "head dW");
+  ck(ctx_, aur::layer_norm_backward(ctx_, A.xs[cfg_.n_layer], A.meanf, A.rstdf, A.lnf_g, A.dln, nullptr,
+                                    A.dx_a, A.g_lnf_g, A.g_lnf_b, A.ln_ws, M, d),
+     "lnf bwd");
+  for (int l = (int)cfg_.n_layer - 1; l >= 0; --l) {
+    Layer& Y = (*layers_)[l];
+    float* dz = A.dx_a;  // gradient w.r.t. this layer's output
+    // FFN (ffn.rs:119-149): dh = (dz · w_proj) ⊙ gelu'(hpre); g_w_proj += dzᵀ·hpost
+    aur::Epilogue gb;
+    gb.mode = aur::EPI_GELU_BWD;
+    gb.X = Y.hpre;
+    ck(ctx_, aur::gemm(ctx_, true, false, dz, d, Y.w_proj, F, A.dh, F, M, F, d, gb), "proj dX");
+    ck(ctx_, aur::gemm(ctx_, false, false, dz, d, Y.hpost, F, Y.g_w_proj, F, d, F, M, true), "proj dW");
+    ck(ctx_, aur::gemm(ctx_, true, false, A.dh, F, Y.w_fc, d, A.dln, d, M, d, F, false), "fc dX");
+    ck(ctx_, aur::gemm(ctx_, false, false, A.dh, F, Y.ln2, d, Y.g_w_fc, d, F, d, M, true), "fc dW");
+    // d_post_attn = dz + LN2'(dln)  (block.rs:207-240)
+    ck(ctx_, aur::layer_norm_backward(ctx_, Y.xmid, Y.mean2, Y.rstd2, Y.ln2_g, A.dln, dz, A.dx_b, Y.g_ln2_g,
+                                      Y.g_ln2_b, A.ln_ws, M, d),
+       "ln2 bwd");
+    float* dpa = A.dx_b;
+    // MHA (transformer/attention.rs:221-334)
+    ck(ctx_, aur::gemm(ctx_, true, false, dpa, d, Y.w_o, d, A.dattn, d, M, d, d, false), "w_o dX");
+    ck(ctx_, aur::gemm(ctx_, false, false, dpa, d, Y.attn, d, Y.g_w_o, d, d, d, M, true), "w_o dW");
+    ck(ctx_, aur_memset0(ctx_, A.dqkv, (size_t)M * 3 * d * sizeof(float)), "zero dqkv");
+    ck(ctx_, aur_mha_bwd_ex(ctx_, Y.qkv, Y.qkv + d, Y.qkv + 2 * d, 3 * d, Y.attn, A.dattn, d, Y.lse, A.dqkv,
+                            A.dqkv + d, A.dqkv + 2 * d, 3 * d, A.attn_ws, b, t, H, dh),
+       "mha_bwd");
+    // dx_q + dx_k + dx_v = dqkv · [w_q; w_k; w_v];  g_w_qkv += dqkvᵀ · ln1
+    ck(ctx_, aur::gemm(ctx_, true, false, A.dqkv, 3 * d, Y.w_qkv, d, A.dln, d, M, d, 3 * d, false), "qkv dX");
+    ck(ctx_, aur::gemm(ctx_, false, false, A.dqkv, 3 * d, Y.ln1, d, Y.g_w_qkv, d, 3 * d, d, M, true),
+       "qkv dW");
+    // dx = d_post_attn + LN1'(dln)
+    ck(ctx_, aur::layer_norm_backward(ctx_, A.xs[l], Y.mean1, Y.rstd1, Y.ln1_g, A.dln, dpa, A.dx_a, Y.g_ln1_g,
+                                      Y.g_ln1_b, A.ln_ws, M, d),
+       "ln1 bwd");
+  }
+  (void)V;
+}
+
+float DecoderTransformerGpu::train_step_batch(const uint32_t* tokens, const uint32_t* targets, uint32_t b,
+                                              uint32_t t) {
+  if (b == 0 || t == 0) return 0.f;
+  if (b > max_batch_ || t > cfg_.seq_len_max) throw Error("train_step_batch: batch/seq too large", AUR_ELIMIT);
+  auto& A = *acts_;
+  const size_t M = (size_t)b * t;
+  upload_tokens(tokens, targets, b, t);
+  // Embedding-gradient scatter plan: rows grouped by token id, ascending.
+  std::vector<int32_t> idx(M);
+  std::iota(idx.begin(), idx.end(), 0);
+  std::stable_sort(idx.begin(), idx.end(), [&](int32_t x, int32_t y) { return tokens[x] < tokens[y]; });
+  std::vector<uint32_t> uniq;
+  std::vector<int32_t> off;
+  for (size_t i = 0; i < M; ++i) {
+    if (i == 0 || tokens[idx[i]] != tokens[idx[i - 1]]) {
+      uniq.push_back(tokens[idx[i]]);
+      off.push_back((int32_t)i);
+    }
+  }
+  off.push_back((int32_t)M);
+  ck(ctx_, aur_h2d(ctx_, A.csr_tok, uniq.data(), uniq.size() * 4), "csr tok");
+  ck(ctx_, aur_h2d(ctx_, A.csr_off, off.data(), off.size() * 4), "csr off");
+  ck(ctx_, aur_h2d(ctx_, A.csr_idx, idx.data(), M * 4), "csr idx");
+
+  encode_forward(b, t, nullptr, true);
+  // CE with 1/T per sequence and the batch mean folded into one scale.
+  ck(ctx_, aur::softmax_ce(ctx_, A.logits, A.tgt, A.nll, (int)M, (int)cfg_.vocab, 1.0f / ((float)t * b)),
+     "softmax_ce");
+  encode_backward(b, t);
+  ck(ctx_, aur::embed_backward(ctx_, A.dx_a, (int)b, (int)t, (int)cfg_.d_model, A.csr_tok, A.csr_off, A.csr_idx,
+                               (int)uniq.size(), A.g_w_tok, A.g_w_pos),
+     "embed bwd");
+  A.nll_host.resize(M);
+  ck(ctx_, aur_d2h(ctx_, A.nll_host.data(), A.nll, M * 4), "download nll");
+  double s = 0.0;
+  for (size_t i = 0; i < M; ++i) s += A.nll_host[i];
+  return (float)(s / t);
+}
+
+void DecoderTransformerGpu::forward(const uint32_t* tokens, uint32_t b, uint32_t t, float* logits_host) {
+  if (b == 0 || t == 0) return;
+  if (b > max_batch_ || t > cfg_.seq_len_max) throw Error("forward: batch/seq too large", AUR_ELIMIT);
+  upload_tokens(tokens, nullptr, b, t);
+  encode_forward(b, t, nullptr, true);
+  if (logits_host)
+    ck(ctx_, aur_d2h(ctx_, logits_host, acts_->logits, (size_t)b * t * cfg_.vocab * 4), "download logits");
+}
+
+float DecoderTransformerGpu::clip_grads(float max_norm) {
+  auto& A = *acts_;
+  ck(ctx_, aur::grad_norm(ctx_, grads_, n_params_, max_norm, A.norm_part, A.stats), "grad norm");
+  ck(ctx_, aur::scale_by(ctx_, grads_, n_params_, A.stats + 1), "clip scale");
+  float nrm = 0.f;
+  ck(ctx_, aur_d2h(ctx_, &nrm, A.stats, 4), "download norm");
+  return nrm;
+}
+
+namespace {
+// bias_correction (src/optimizer.rs:86-90): 1 − β^t with f32 powi.
+inline float powi_f(float b, uint64_t e) {
+  float r = 1.0f;
+  for (uint64_t i = 0; i < e; ++i) r *= b;
+  return r;
+}
+}  // namespace
+
+void DecoderTransformerGpu::step_adamw(const AdamWConfig& c) {
+  step += 1;
+  const float bc1 = 1.0f - powi_f(c.beta1, step), bc2 = 1.0f - powi_f(c.beta2, step);
+  ck(ctx_, aur::adamw(ctx_, params_, grads_, m1_, m2_, n_params_, n_decay_, nullptr, c.lr, c.beta1, c.beta2,
+                      c.eps, c.weight_decay, bc1, bc2),
+     "adamw");
+}
+
+float DecoderTransformerGpu::clip_and_step_adamw(float max_norm, const AdamWConfig& c) {
+  auto& A = *acts_;
+  ck(ctx_, aur::grad_norm(ctx_, grads_, n_params_, max_norm, A.norm_part, A.stats), "grad norm");
+  step += 1;
+  const float bc1 = 1.0f - powi_f(c.beta1, step), bc2 = 1.0f - powi_f(c.beta2, step);
+  ck(ctx_, aur::adamw(ctx_, params_, grads_, m1_, m2_, n_params_, n_decay_, A.stats + 1, c.lr, c.beta1,
+                      c.beta2, c.eps, c.weight_decay, bc1, bc2),
+     "adamw");
+  float nrm = 0.f;
+  ck(ctx_, aur_d2h(ctx_, &nrm, A.stats, 4), "download norm");
+  return nrm;
+}
+
+// ------------------------------------------------------------------ KV cache
+
+KvCacheGpu::KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch_, uint32_t max_len_)
+    : batch(batch_), max_len(max_len_), d_model(model.config().d_model), n_layer(model.config().n_layer),
+      ctx_(model.ctx()) {
+  const auto& c = model.config();
+  if (batch == 0 || max_len == 0 || max_len > c.seq_len_max)
+    throw Error("KvCacheGpu: batch > 0 and 0 < max_len <= seq_len_max required", AUR_EINVAL);
+  const size_t B = batch, d = d_model, F = c.d_ff, V = c.vocab;
+  const size_t hist = (size_t)n_layer * B * max_len * d;
+  const size_t scratch = (aur_mha_kv_ws_bytes(batch, c.n_head, max_len) + 3) / 4;
+  // x, ln, qkv (3), attn, xmid = 7 rows of d per sequence
+  const size_t floats = 2 * hist + B * (d * 7 + 2 * F + V) + scratch;
+  bytes_ = floats * 4 + 3 * B * 4 + 32 * 256;
+  ck(ctx_, aur_malloc(ctx_, bytes_, &mem_), "KvCacheGpu alloc");
+  Carver cv{static_cast<char*>(mem_)};
+  k_ = cv.take<float>(hist);
+  v_ = cv.take<float>(hist);
+  x_ = cv.take<float>(B * d);
+  ln_ = cv.take<float>(B * d);
+  qkv_ = cv.take<float>(3 * B * d);
+  attn_ = cv.take<float>(B * d);
+  xmid_ = cv.take<float>(B * d);
+  hpre_ = cv.take<float>(B * F);
+  hpost_ = cv.take<float>(B * F);
+  logits_ = cv.take<float>(B * V);
+  scratch_ = cv.take<float>(scratch);
+  pos_ = cv.take<int32_t>(B);
+  lens_ = cv.take<int32_t>(B);
+  tok_ = cv.take<uint32_t>(B);
+  if (cv.off > bytes_) throw Error("KvCacheGpu: arena overflow", AUR_ENOMEM);
+  reset();
+}
+
+KvCacheGpu::~KvCacheGpu() {
+  if (mem_) aur_free(ctx_, mem_);
+}
+
+void KvCacheGpu::reset() {
+  ck(ctx_, aur_memset0(ctx_, mem_, bytes_), "KvCacheGpu reset");
+  current_len = 0;
+}
+
+void DecoderTransformerGpu::prefill_kv(KvCacheGpu& cache, const uint32_t* tokens, uint32_t b, uint32_t t,
+                                       float* last_logits) {
+  if (b != cache.batch) throw Error("prefill_kv: batch differs from the cache's", AUR_EINVAL);
+  if (t == 0 || t > cache.max_len || b > max_batch_) throw Error("prefill_kv: bad length", AUR_EINVAL);
+  cache.reset();
+  upload_tokens(tokens, nullptr, b, t);
+  encode_forward(b, t, &cache, false);
+  auto& A = *acts_;
+  const size_t V = cfg_.vocab;
+  ck(ctx_, aur_d2d(ctx_, cache.logits_, A.logits, (size_t)b * V * 4), "prefill logits");
+  ck(ctx_, aur::argmax_rows(ctx_, cache.logits_, (int)b, (int)V, cache.tok_), "prefill argmax");
+  std::vector<int32_t> pos(b, (int32_t)t);
+  ck(ctx_, aur_h2d(ctx_, cache.pos_, pos.data(), b * 4), "prefill pos");
+  cache.current_len = t;
+  if (last_logits) ck(ctx_, aur_d2h(ctx_, last_logits, cache.logits_, (size_t)b * V * 4), "download logits");
+}
+
+void DecoderTransformerGpu::generate_step_kv(KvCacheGpu& cache, const uint32_t* tokens, float* logits_host,
+                                             uint32_t* next_tokens_host) {
+  if (cache.current_len >= cache.max_len) throw Error("generate_step_kv: cache full", AUR_ELIMIT);
+  auto& A = *acts_;
+  const int B = (int)cache.batch, d = (int)cfg_.d_model, F = (int)cfg_.d_ff, V = (int)cfg_.vocab;
+  const int H = (int)cfg_.n_head, dh = d / H;
+  if (tokens) {
+    for (int i = 0; i < B; ++i)
+      if (tokens[i] >= cfg_.vocab) throw Error("token id out of vocab", AUR_EINVAL);
+    ck(ctx_, aur_h2d(ctx_, cache.tok_, tokens, (size_t)B * 4), "upload step tokens");
+  }
+  // h = w_tok[tok] + w_pos[pos]  (kv_cache.rs:103-115)
+  ck(ctx_, aur::embed_forward(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, 0, cache.x_, B, d), "embed");
+  ck(ctx_, aur::lens_from_pos(ctx_, cache.pos_, cache.lens_, B), "lens");
+  const int t_max = (int)cache.current_len + 1;
+  for (uint32_t l = 0; l < cfg_.n_layer; ++l) {
+    Layer& Y = (*layers_)[l];
+    // block_step (kv_cache.rs:147-245) for B sequences at once
+    ck(ctx_, aur::layer_norm_forward(ctx_, cache.x_, Y.ln1_g, Y.ln1_b, cache.ln_, nullptr, nullptr, B, d,
+                                     kLnEps),
+       "ln1");
+    ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, Y.w_qkv, d, cache.qkv_, 3 * d, B, 3 * d, d, false), "qkv");
+    ck(ctx_, aur::kv_store(ctx_, cache.qkv_, d, cache.k_history(l), cache.v_history(l), (int)cache.max_len,
+                           cache.pos_, B, 0),
+       "kv append");
+    ck(ctx_, aur::mha_kv_batched(ctx_, cache.qkv_, 3 * d, cache.k_history(l), cache.v_history(l), cache.attn_,
+                                 cache.scratch_, cache.lens_, t_max, B, H, dh, (int)cache.max_len),
+       "mha_kv");
+    aur::Epilogue resid;
+    resid.mode = aur::EPI_RESID;
+    resid.R = cache.x_;
+    ck(ctx_, aur::gemm(ctx_, true, true, cache.attn_, d, Y.w_o, d, cache.xmid_, d, B, d, d, resid), "w_o");
+    ck(ctx_, aur::layer_norm_forward(ctx_, cache.xmid_, Y.ln2_g, Y.ln2_b, cache.ln_, nullptr, nullptr, B, d,
+                                     kLnEps),
+       "ln2");
+    aur::Epilogue ge;
+    ge.mode = aur::EPI_GELU;
+    ge.C2 = cache.hpost_;
+    ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, Y.w_fc, d, cache.hpre_, F, B, F, d, ge), "w_fc");
+    aur::Epilogue r2;
+    r2.mode = aur::EPI_RESID;
+    r2.R = cache.xmid_;
+    ck(ctx_, aur::gemm(ctx_, true, true, cache.hpost_, F, Y.w_proj, F, cache.x_, d, B, d, F, r2), "w_proj");
+  }
+  ck(ctx_, aur::layer_norm_forward(ctx_, cache.x_, A.lnf_g, A.lnf_b, cache.ln_, nullptr, nullptr, B, d, kLnEps),
+     "lnf");
+  ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, A.w_tok, d, cache.logits_, V, B, V, d, false), "head");
+  ck(ctx_, aur::argmax_rows(ctx_, cache.logits_, B, V, cache.tok_), "argmax");
+  ck(ctx_, aur::advance_pos(ctx_, cache.pos_, B), "advance pos");
+  cache.current_len += 1;
+  if (logits_host) ck(ctx_, aur_d2h(ctx_, logits_host, cache.logits_, (size_t)B * V * 4), "download logits");
+  if (next_tokens_host) ck(ctx_, aur_d2h(ctx_, next_tokens_host, cache.tok_, (size_t)B * 4), "download tokens");
+}
+
+}  // namespace aurora
+
+// ---------------------------------------------------------------- C ABI
+using aurora::DecoderTransformerGpu;
+using aurora::KvCacheGpu;
+
+struct aur_model {
+  DecoderTransformerGpu* m;
+};
+struct aur_kv_cache {
+  KvCacheGpu* c;
+  aur_model* owner;
+};
+
+namespace {
+template <class F>
+int guard(aur_ctx* ctx, F&& f) {
+  try {
+    f();
+    return 0;
+  } catch (const aurora::Error& e) {
+    if (ctx) ctx->last_error = e.what();
+    return e.code ? e.code : AUR_EINVAL;
+  } catch (const std::exception& e) {
+    if (ctx) ctx->last_error = e.what();
+    return AUR_EINVAL;
+  }
+}
+}  // namespace
+
+extern "C" {
+
+int aur_model_create(aur_ctx* ctx, const aur_model_config* cfg, uint32_t max_batch, aur_model** out) {
+  AUR_CHECK_CTX(ctx);
+  if (!cfg || !out) return aur::set_error(ctx, AUR_EINVAL, "aur_model_create: null argument");
+  *out = nullptr;
+  return guard(ctx, [&] {
+    aurora::TransformerConfig c{cfg->vocab, cfg->d_model, cfg->n_layer, cfg->n_head, cfg->d_ff, cfg->seq_len_max};
+    auto* m = new aur_model{new DecoderTransformerGpu(ctx, c, max_batch)};
+    *out = m;
+  });
+}
+
+int aur_model_destroy(aur_model* m) {
+  if (!m) return 0;
+  delete m->m;
+  delete m;
+  return 0;
+}
+
+int aur_model_tensor(aur_model* m, const char* name, int32_t layer, int32_t grad, float** ptr, size_t* len) {
+  if (!m || !name || !ptr) return AUR_EINVAL;
+  float* p = m->m->tensor(name, layer, grad != 0, len);
+  *ptr = p;
+  if (!p) return aur::set_error(m->m->ctx(), AUR_EINVAL, "aur_model_tensor: unknown tensor %s[%d]", name, layer);
+  return 0;
+}
+
+int aur_model_zero_grad(aur_model* m) {
+  if (!m) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] { m->m->zero_grad(); });
+}
+
+int aur_model_train_step_batch(aur_model* m, const uint32_t* tokens, const uint32_t* targets, uint32_t b,
+                               uint32_t t, float* loss_sum) {
+  if (!m || !tokens || !targets) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] {
+    float l = m->m->train_step_batch(tokens, targets, b, t);
+    if (loss_sum) *loss_sum = l;
+  });
+}
+
+int aur_model_forward(aur_model* m, const uint32_t* tokens, uint32_t b, uint32_t t, float* logits) {
+  if (!m || !tokens) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] { m->m->forward(tokens, b, t, logits); });
+}
+
+int aur_model_clip_grads(aur_model* m, float max_norm, float* norm) {
+  if (!m) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] {
+    float n = m->m->clip_grads(max_norm);
+    if (norm) *norm = n;
+  });
+}
+
+int aur_model_step_adamw(aur_model* m, float lr, float beta1, float beta2, float eps, float weight_decay) {
+  if (!m) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] { m->m->step_adamw(aurora::AdamWConfig{lr, beta1, beta2, eps, weight_decay}); });
+}
+
+int aur_model_clip_step_adamw(aur_model* m, float max_norm, float lr, float beta1, float beta2, float eps,
+                              float weight_decay, float* norm) {
+  if (!m) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] {
+    float n = m->m->clip_and_step_adamw(max_norm, aurora::AdamWConfig{lr, beta1, beta2, eps, weight_decay});
+    if (norm) *norm = n;
+  });
+}
+
+int aur_kv_cache_create(aur_model* m, uint32_t batch, uint32_t max_len, aur_kv_cache** out) {
+  if (!m || !out) return AUR_EINVAL;
+  *out = nullptr;
+  return guard(m->m->ctx(), [&] { *out = new aur_kv_cache{new KvCacheGpu(*m->m, batch, max_len), m}; });
+}
+
+int aur_kv_cache_reset(aur_kv_cache* c) {
+  if (!c) return AUR_EINVAL;
+  return guard(c->owner->m->ctx(), [&] { c->c->reset(); });
+}
+
+int aur_kv_cache_destroy(aur_kv_cache* c) {
+  if (!c) return 0;
+  delete c->c;
+  delete c;
+  return 0;
+}
+
+int aur_kv_cache_len(aur_kv_cache* c, uint32_t* len) {
+  if (!c || !len) return AUR_EINVAL;
+  *len = c->c->current_len;
+  return 0;
+}
+
+int aur_kv_cache_history(aur_kv_cache* c, uint32_t layer, float** k, float** v) {
+  if (!c || !k || !v || layer >= c->c->n_layer) return AUR_EINVAL;
+  *k = c->c->k_history(layer);
+  *v = c->c->v_history(layer);
+  return 0;
+}
+
+int aur_model_prefill_kv(aur_model* m, aur_kv_cache* c, const uint32_t* tokens, uint32_t b, uint32_t t,
+                         float* last_logits) {
+  if (!m || !c || !tokens) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] { m->m->prefill_kv(*c->c, tokens, b, t, last_logits); });
+}
+
+int aur_model_generate_step(aur_model* m, aur_kv_cache* c, const uint32_t* tokens, float* logits,
+                            uint32_t* next_tokens) {
+  if (!m || !c) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] { m->m->generate_step_kv(*c->c, tokens, logits, next_tokens); });
+}
+
+int aur_model_generate_greedy(aur_model* m, aur_kv_cache* c, uint32_t n_steps, uint32_t* out_tokens) {
+  if (!m || !c) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] {
+    const uint32_t B = c->c->batch;
+    for (uint32_t s = 0; s < n_steps; ++s)
+      m->m->generate_step_kv(*c->c, nullptr, nullptr, out_tokens ? out_tokens + (size_t)s * B : nullptr);
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,478 @@
+// Step-support kernels around the GEMM / attention hot path: everything one
+// training step (embed → blocks → LN → tied head → CE → backward → clip →
+// AdamW) and one KV-cache decode step need besides the matrix products.
+// All reductions have a fixed order (no atomics), so a step is bitwise
+// reproducible run to run.  These are bandwidth-bound elementwise / row
+// kernels: one wave per row, float4 traffic where the row allows it.
+//
+// Reference semantics: LN src/attention.rs:84-157 (eps 1e-5, biased
+// variance), softmax-CE src/transformer/model.rs:820-858, embedding
+// src/transformer/embedding.rs:95-142, clip model.rs:1011-1017 with the
+// L2 norm of model.rs:442-500, AdamW src/optimizer.rs:58-90.
+#include "common.hpp"
+#include "step_ops.hpp"
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// Block-wide sum for 256 threads; every thread gets the result.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// ---------------------------------------------------------------- embedding
+// out[r, :] = w_tok[tok[r], :] + w_pos[pos(r), :],  pos(r) = pos_dev ? pos_dev[r] : r % T.
+__global__ void __launch_bounds__(256) embed_fwd_kernel(const float* __restrict__ w_tok,
+                                                        const float* __restrict__ w_pos,
+                                                        const uint32_t* __restrict__ tok,
+                                                        const int32_t* __restrict__ pos_dev, int T,
+                                                        float* __restrict__ out, int rows, int d) {
+  const int r = blockIdx.x;
+  if (r >= rows) return;
+  const int p = pos_dev ? pos_dev[r] : r % T;
+  const float* a = w_tok + (size_t)tok[r] * d;
+  const float* b = w_pos + (size_t)p * d;
+  float* o = out + (size_t)r * d;
+  for (int c = threadIdx.x; c < d; c += blockDim.x) o[c] = a[c] + b[c];
+}
+
+// g_w_tok[v, :] += Σ_{r ∈ rows(v)} dy[r, :] with rows(v) ascending (CSR built
+// on the host from the token ids: tok_ids[u], row_off[u]..row_off[u+1]).
+__global__ void __launch_bounds__(256) embed_tok_bwd_kernel(const float* __restrict__ dy,
+                                                            const uint32_t* __restrict__ tok_ids,
+                                                            const int32_t* __restrict__ row_off,
+                                                            const int32_t* __restrict__ row_idx,
+                                                            float* __restrict__ g_w_tok, int d) {
+  const int u = blockIdx.x;
+  const int beg = row_off[u], end = row_off[u + 1];
+  float* g = g_w_tok + (size_t)tok_ids[u] * d;
+  for (int c = threadIdx.x; c < d; c += blockDim.x) {
+    float s = 0.f;
+    for (int i = beg; i < end; ++i) s += dy[(size_t)row_idx[i] * d + c];
+    g[c] += s;
+  }
+}
+
+// g_w_pos[t, :] += Σ_b dy[b*T + t, :], b ascending.
+__global__ void __launch_bounds__(256) embed_pos_bwd_kernel(const float* __restrict__ dy, int B, int T,
+                                                            float* __restrict__ g_w_pos, int d) {
+  const int t = blockIdx.x;
+  float* g = g_w_pos + (size_t)t * d;
+  for (int c = threadIdx.x; c < d; c += blockDim.x) {
+    float s = 0.f;
+    for (int b = 0; b < B; ++b) s += dy[((size_t)b * T + t) * d + c];
+    g[c] += s;
+  }
+}
+
+// ---------------------------------------------------------------- layer norm
+// One wave per row: mu = Σx/d, var = Σ(x−mu)²/d, s = 1/sqrt(var + eps),
+// y = (x − mu)·s·γ + β.  Saves mean and s for the backward.
+__global__ void __launch_bounds__(256) ln_fwd_kernel(const float* __restrict__ x,
+                                                     const float* __restrict__ gamma,
+                                                     const float* __restrict__ beta,
+                                                     float* __restrict__ y, float* __restrict__ mean,
+                                                     float* __restrict__ rstd, int rows, int d,
+                                                     float eps) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float* xr = x + (size_t)r * d;
+  float s = 0.f;
+  for (int c = lane; c < d; c += 64) s += xr[c];
+  const float mu = wave_sum(s) / (float)d;
+  float v = 0.f;
+  for (int c = lane; c < d; c += 64) {
+    const float t = xr[c] - mu;
+    v += t * t;
+  }
+  const float var = wave_sum(v) / (float)d;
+  const float is = 1.0f / sqrtf(var + eps);
+  float* yr = y + (size_t)r * d;
+  for (int c = lane; c < d; c += 64) yr[c] = (xr[c] - mu) * is * gamma[c] + beta[c];
+  if (lane == 0) {
+    if (mean) mean[r] = mu;
+    if (rstd) rstd[r] = is;
+  }
+}
+
+// dx = s·(g − (Σg + x̂·Σ(g·x̂))/d) [+ dres],  g = dy·γ,  x̂ = (x − mu)·s.
+__global__ void __launch_bounds__(256) ln_bwd_kernel(const float* __restrict__ x,
+                                                     const float* __restrict__ mean,
+                                                     const float* __restrict__ rstd,
+                                                     const float* __restrict__ gamma,
+                                                     const float* __restrict__ dy,
+                                                     const float* __restrict__ dres,
+                                                     float* __restrict__ dx, int rows, int d) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float mu = mean[r], s = rstd[r];
+  const float* xr = x + (size_t)r * d;
+  const float* dyr = dy + (size_t)r * d;
+  float sg = 0.f, sgx = 0.f;
+  for (int c = lane; c < d; c += 64) {
+    const float g = dyr[c] * gamma[c];
+    sg += g;
+    sgx += g * ((xr[c] - mu) * s);
+  }
+  sg = wave_sum(sg);
+  sgx = wave_sum(sgx);
+  const float inv_d = 1.0f / (float)d;
+  float* dxr = dx + (size_t)r * d;
+  const float* dr = dres ? dres + (size_t)r * d : nullptr;
+  for (int c = lane; c < d; c += 64) {
+    const float g = dyr[c] * gamma[c];
+    const float xh = (xr[c] - mu) * s;
+    float v = s * (g - inv_d * (sg + xh * sgx));
+    if (dr) v += dr[c];
+    dxr[c] = v;
+  }
+}
+
+// Partial column sums over a chunk of rows: pg[chunk][c] = Σ dy·x̂, pb = Σ dy.
+constexpr int LN_CHUNK = 64;
+__global__ void __launch_bounds__(256) ln_param_partial_kernel(const float* __restrict__ x,
+                                                               const float* __restrict__ mean,
+                                                               const float* __restrict__ rstd,
+                                                               const float* __restrict__ dy,
+                                                               float* __restrict__ pg,
+                                                               float* __restrict__ pb, int rows,
+                                                               int d) {
+  const int chunk = blockIdx.y;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= d) return;
+  const int r0 = chunk * LN_CHUNK, r1 = min(rows, r0 + LN_CHUNK);
+  float sgm = 0.f, sb = 0.f;
+  for (int r = r0; r < r1; ++r) {
+    const float g = dy[(size_t)r * d + c];
+    sgm += g * ((x[(size_t)r * d + c] - mean[r]) * rstd[r]);
+    sb += g;
+  }
+  pg[(size_t)chunk * d + c] = sgm;
+  pb[(size_t)chunk * d + c] = sb;
+}
+
+// dγ[c] += Σ_chunk pg[chunk][c], dβ[c] += Σ_chunk pb[chunk][c] (chunk ascending).
+__global__ void __launch_bounds__(256) ln_param_final_kernel(const float* __restrict__ pg,
+                                                             const float* __restrict__ pb,
+                                                             int nchunks, float* __restrict__ dgamma,
+                                                             float* __restrict__ dbeta, int d) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= d) return;
+  float sg = 0.f, sb = 0.f;
+  for (int k = 0; k < nchunks; ++k) {
+    sg += pg[(size_t)k * d + c];
+    sb += pb[(size_t)k * d + c];
+  }
+  dgamma[c] += sg;
+  dbeta[c] += sb;
+}
+
+// ---------------------------------------------------------------- softmax-CE
+// In place: logits row → (softmax − onehot(target))·scale, and
+// nll[r] = −ln(max(p_target, 1e-12)).
+__global__ void __launch_bounds__(256) softmax_ce_kernel(float* __restrict__ logits,
+                                                         const uint32_t* __restrict__ targets,
+                                                         float* __restrict__ nll, int V,
+                                                         float scale) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  float* row = logits + (size_t)r * V;
+  float mx = -INFINITY;
+  for (int c = threadIdx.x; c < V; c += 256) mx = fmaxf(mx, row[c]);
+  mx = block_max(mx, red);
+  float s = 0.f;
+  for (int c = threadIdx.x; c < V; c += 256) {
+    const float e = expf(row[c] - mx);
+    row[c] = e;
+    s += e;
+  }
+  s = block_sum(s, red);
+  const float inv = 1.0f / s;
+  const uint32_t tgt = targets[r];
+  __syncthreads();
+  if (threadIdx.x == 0) nll[r] = -logf(fmaxf(row[tgt] * inv, 1e-12f));
+  __syncthreads();
+  for (int c = threadIdx.x; c < V; c += 256) {
+    float g = row[c] * inv;
+    if ((uint32_t)c == tgt) g -= 1.0f;
+    row[c] = g * scale;
+  }
+}
+
+// ---------------------------------------------------------- grad norm / clip
+// Deterministic two-stage Σ g²: fixed-size blocks, then one block in order.
+__global__ void __launch_bounds__(256) sumsq_partial_kernel(const float* __restrict__ g, size_t n,
+                                                            float* __restrict__ part) {
+  __shared__ float red[4];
+  const size_t per = (n + gridDim.x - 1) / gridDim.x;
+  const size_t beg = (size_t)blockIdx.x * per, end = min(n, beg + per);
+  float s = 0.f;
+  for (size_t i = beg + threadIdx.x; i < end; i += 256) s += g[i] * g[i];
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+
+// stats[0] = ‖g‖₂, stats[1] = clip factor (max_norm/‖g‖ if ‖g‖ > max_norm > 0, else 1).
+__global__ void __launch_bounds__(256) norm_final_kernel(const float* __restrict__ part, int nparts,
+                                                         float max_norm, float* __restrict__ stats) {
+  __shared__ float red[4];
+  float s = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += 256) s += part[i];
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) {
+    const float nrm = sqrtf(s);
+    stats[0] = nrm;
+    stats[1] = (max_norm > 0.f && nrm > max_norm && nrm > 0.f) ? max_norm / nrm : 1.0f;
+  }
+}
+
+// ---------------------------------------------------------------- AdamW
+// Elements [0, n_decay) get decoupled weight decay, [n_decay, n) do not.
+// The gradient is multiplied by *clip (the clip factor) on the fly, which
+// equals the reference's in-place grads.scale(max/‖g‖) before the update.
+__global__ void __launch_bounds__(256) adamw_kernel(float* __restrict__ p, const float* __restrict__ g,
+                                                    float* __restrict__ m1, float* __restrict__ m2,
+                                                    size_t n, size_t n_decay,
+                                                    const float* __restrict__ clip, float lr,
+                                                    float b1, float b2, float eps, float wd, float bc1,
+                                                    float bc2) {
+  const float cf = clip ? *clip : 1.0f;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float gi = cf == 1.0f ? g[i] : g[i] * cf;
+    const float a = b1 * m1[i] + (1.0f - b1) * gi;
+    const float b = b2 * m2[i] + (1.0f - b2) * gi * gi;
+    m1[i] = a;
+    m2[i] = b;
+    const float mh = a / bc1, vh = b / bc2;
+    float step = lr * mh / (sqrtf(vh) + eps);
+    if (i < n_decay) step += lr * wd * p[i];
+    p[i] -= step;
+  }
+}
+
+__global__ void __launch_bounds__(256) scale_kernel(float* __restrict__ x, size_t n,
+                                                    const float* __restrict__ f) {
+  const float cf = *f;
+  if (cf == 1.0f) return;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] *= cf;
+}
+
+// ------------------------------------------------------------------ KV cache
+// Copies the k and v parts of qkv rows into the per-sequence history:
+//   hist[b, pos, :] = qkv[row, d:2d] / qkv[row, 2d:3d]
+// decode: row = b, pos = pos_dev[b];  prefill: row = b*T + t, pos = t.
+__global__ void __launch_bounds__(256) kv_store_kernel(const float* __restrict__ qkv, int d,
+                                                       float* __restrict__ kh, float* __restrict__ vh,
+                                                       int max_len, const int32_t* __restrict__ pos_dev,
+                                                       int T) {
+  const int row = blockIdx.x;
+  int b, pos;
+  if (pos_dev) {
+    b = row;
+    pos = pos_dev[row];
+  } else {
+    b = row / T;
+    pos = row % T;
+  }
+  const float* src = qkv + (size_t)row * 3 * d;
+  float* kd = kh + ((size_t)b * max_len + pos) * d;
+  float* vd = vh + ((size_t)b * max_len + pos) * d;
+  for (int c = threadIdx.x; c < d; c += 256) {
+    kd[c] = src[d + c];
+    vd[c] = src[2 * d + c];
+  }
+}
+
+// lens[b] = pos[b] + 1 (attention length after appending position pos[b]).
+__global__ void lens_from_pos_kernel(const int32_t* __restrict__ pos, int32_t* __restrict__ lens, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B) lens[b] = pos[b] + 1;
+}
+
+__global__ void advance_pos_kernel(int32_t* __restrict__ pos, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B) pos[b] += 1;
+}
+
+// First index of the row maximum (src/transformer/loss.rs argmax: strict >).
+__global__ void __launch_bounds__(256) argmax_kernel(const float* __restrict__ logits, int V,
+                                                     uint32_t* __restrict__ out) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int r = blockIdx.x;
+  const float* row = logits + (size_t)r * V;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int c = threadIdx.x; c < V; c += 256) {
+    const float v = row[c];
+    if (v > best) {
+      best = v;
+      bi = c;
+    }
+  }
+  sv[threadIdx.x] = best;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = 128; s >= 1; s >>= 1) {
+    if (threadIdx.x < s) {
+      const float ov = sv[threadIdx.x + s];
+      const int oi = si[threadIdx.x + s];
+      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[r] = (uint32_t)(si[0] == 0x7fffffff ? 0 : si[0]);
+}
+
+__global__ void gather_rows_kernel(const float* __restrict__ src, int ld_src, int row_step,
+                                   int row_off, float* __restrict__ dst, int rows, int d) {
+  const int r = blockIdx.x;
+  if (r >= rows) return;
+  const float* s = src + ((size_t)r * row_step + row_off) * ld_src;
+  float* o = dst + (size_t)r * d;
+  for (int c = threadIdx.x; c < d; c += 256) o[c] = s[c];
+}
+
+unsigned grid_1d(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 16384); }
+
+}  // namespace
+
+namespace aur {
+
+#define LAUNCH_OK(ctx, name) AUR_LAUNCH_CHECK(ctx, name); return 0
+
+int embed_forward(aur_ctx* ctx, const float* w_tok, const float* w_pos, const uint32_t* tok,
+                  const int32_t* pos_dev, int T, float* out, int rows, int d) {
+  hipLaunchKernelGGL(embed_fwd_kernel, dim3(rows), dim3(256), 0, ctx->stream, w_tok, w_pos, tok, pos_dev,
+                     T, out, rows, d);
+  LAUNCH_OK(ctx, "embed_fwd_kernel");
+}
+
+int embed_backward(aur_ctx* ctx, const float* dy, int B, int T, int d, const uint32_t* tok_ids,
+                   const int32_t* row_off, const int32_t* row_idx, int n_unique, float* g_w_tok,
+                   float* g_w_pos) {
+  if (n_unique > 0)
+    hipLaunchKernelGGL(embed_tok_bwd_kernel, dim3(n_unique), dim3(256), 0, ctx->stream, dy, tok_ids,
+                       row_off, row_idx, g_w_tok, d);
+  hipLaunchKernelGGL(embed_pos_bwd_kernel, dim3(T), dim3(256), 0, ctx->stream, dy, B, T, g_w_pos, d);
+  LAUNCH_OK(ctx, "embed_bwd kernels");
+}
+
+int layer_norm_forward(aur_ctx* ctx, const float* x, const float* gamma, const float* beta, float* y,
+                       float* mean, float* rstd, int rows, int d, float eps) {
+  hipLaunchKernelGGL(ln_fwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, ctx->stream, x, gamma, beta, y,
+                     mean, rstd, rows, d, eps);
+  LAUNCH_OK(ctx, "ln_fwd_kernel");
+}
+
+size_t layer_norm_backward_ws_floats(int rows, int d) {
+  return 2 * (size_t)((rows + LN_CHUNK - 1) / LN_CHUNK) * d;
+}
+
+int layer_norm_backward(aur_ctx* ctx, const float* x, const float* mean, const float* rstd,
+                        const float* gamma, const float* dy, const float* dres, float* dx,
+                        float* dgamma, float* dbeta, float* ws, int rows, int d) {
+  hipLaunchKernelGGL(ln_bwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, ctx->stream, x, mean, rstd, gamma,
+                     dy, dres, dx, rows, d);
+  const int nch = (rows + LN_CHUNK - 1) / LN_CHUNK;
+  float* pg = ws;
+  float* pb = ws + (size_t)nch * d;
+  hipLaunchKernelGGL(ln_param_partial_kernel, dim3((d + 255) / 256, nch), dim3(256), 0, ctx->stream, x,
+                     mean, rstd, dy, pg, pb, rows, d);
+  hipLaunchKernelGGL(ln_param_final_kernel, dim3((d + 255) / 256), dim3(256), 0, ctx->stream, pg, pb, nch,
+                     dgamma, dbeta, d);
+  LAUNCH_OK(ctx, "ln_bwd kernels");
+}
+
+int softmax_ce(aur_ctx* ctx, float* logits, const uint32_t* targets, float* nll, int rows, int V,
+               float scale) {
+  hipLaunchKernelGGL(softmax_ce_kernel, dim3(rows), dim3(256), 0, ctx->stream, logits, targets, nll, V,
+                     scale);
+  LAUNCH_OK(ctx, "softmax_ce_kernel");
+}
+
+constexpr int kNormParts = 1024;
+
+int grad_norm(aur_ctx* ctx, const float* g, size_t n, float max_norm, float* part, float* stats) {
+  hipLaunchKernelGGL(sumsq_partial_kernel, dim3(kNormParts), dim3(256), 0, ctx->stream, g, n, part);
+  hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(256), 0, ctx->stream, part, kNormParts, max_norm,
+                     stats);
+  LAUNCH_OK(ctx, "grad norm kernels");
+}
+
+size_t grad_norm_ws_floats() { return kNormParts; }
+
+int scale_by(aur_ctx* ctx, float* x, size_t n, const float* factor) {
+  hipLaunchKernelGGL(scale_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, x, n, factor);
+  LAUNCH_OK(ctx, "scale_kernel");
+}
+
+int adamw(aur_ctx* ctx, float* p, const float* g, float* m1, float* m2, size_t n, size_t n_decay,
+          const float* clip, float lr, float b1, float b2, float eps, float wd, float bc1, float bc2) {
+  hipLaunchKernelGGL(adamw_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, p, g, m1, m2, n, n_decay,
+                     clip, lr, b1, b2, eps, wd, bc1, bc2);
+  LAUNCH_OK(ctx, "adamw_kernel");
+}
+
+int kv_store(aur_ctx* ctx, const float* qkv, int d, float* kh, float* vh, int max_len,
+             const int32_t* pos_dev, int rows, int T) {
+  hipLaunchKernelGGL(kv_store_kernel, dim3(rows), dim3(256), 0, ctx->stream, qkv, d, kh, vh, max_len,
+                     pos_dev, T);
+  LAUNCH_OK(ctx, "kv_store_kernel");
+}
+
+int lens_from_pos(aur_ctx* ctx, const int32_t* pos, int32_t* lens, int B) {
+  hipLaunchKernelGGL(lens_from_pos_kernel, dim3((B + 255) / 256), dim3(256), 0, ctx->stream, pos, lens, B);
+  LAUNCH_OK(ctx, "lens_from_pos_kernel");
+}
+
+int advance_pos(aur_ctx* ctx, int32_t* pos, int B) {
+  hipLaunchKernelGGL(advance_pos_kernel, dim3((B + 255) / 256), dim3(256), 0, ctx->stream, pos, B);
+  LAUNCH_OK(ctx, "advance_pos_kernel");
+}
+
+int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, ctx->stream, logits, V, out);
+  LAUNCH_OK(ctx, "argmax_kernel");
+}
+
+int gather_rows(aur_ctx* ctx, const float* src, int ld_src, int row_step, int row_off, float* dst,
+                int rows, int d) {
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(rows), dim3(256), 0, ctx->stream, src, ld_src, row_step,
+                     row_off, dst, rows, d);
+  LAUNCH_OK(ctx, "gather_rows_kernel");
+}
+
+}  // namespace aur

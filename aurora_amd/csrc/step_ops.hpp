@@ -1,0 +1,51 @@
+// Launchers of the step-support kernels (step_ops.hip).  All enqueue on the
+// context's stream and return 0 or an error code.
+#pragma once
+
+#include "common.hpp"
+
+namespace aur {
+
+// out[r] = w_tok[tok[r]] + w_pos[pos(r)], pos(r) = pos_dev ? pos_dev[r] : r % T.
+int embed_forward(aur_ctx* ctx, const float* w_tok, const float* w_pos, const uint32_t* tok,
+                  const int32_t* pos_dev, int T, float* out, int rows, int d);
+// g_w_tok[tok_ids[u]] += Σ dy[row_idx[row_off[u]..row_off[u+1])]; g_w_pos[t] += Σ_b dy[b*T+t].
+int embed_backward(aur_ctx* ctx, const float* dy, int B, int T, int d, const uint32_t* tok_ids,
+                   const int32_t* row_off, const int32_t* row_idx, int n_unique, float* g_w_tok,
+                   float* g_w_pos);
+
+int layer_norm_forward(aur_ctx* ctx, const float* x, const float* gamma, const float* beta, float* y,
+                       float* mean, float* rstd, int rows, int d, float eps);
+size_t layer_norm_backward_ws_floats(int rows, int d);
+// dx = LN'(dy) [+ dres]; dgamma/dbeta accumulated (fixed-order column sums in ws).
+int layer_norm_backward(aur_ctx* ctx, const float* x, const float* mean, const float* rstd,
+                        const float* gamma, const float* dy, const float* dres, float* dx,
+                        float* dgamma, float* dbeta, float* ws, int rows, int d);
+
+// In place: logits → (softmax − onehot)·scale; nll[r] per row.
+int softmax_ce(aur_ctx* ctx, float* logits, const uint32_t* targets, float* nll, int rows, int V,
+               float scale);
+
+// stats[0] = ‖g‖₂ over n floats, stats[1] = clip factor for max_norm.
+int grad_norm(aur_ctx* ctx, const float* g, size_t n, float max_norm, float* part, float* stats);
+size_t grad_norm_ws_floats();
+int scale_by(aur_ctx* ctx, float* x, size_t n, const float* factor);
+int adamw(aur_ctx* ctx, float* p, const float* g, float* m1, float* m2, size_t n, size_t n_decay,
+          const float* clip, float lr, float b1, float b2, float eps, float wd, float bc1, float bc2);
+
+// K/V rows of a fused qkv [rows, 3d] into the history [B, max_len, d].
+int kv_store(aur_ctx* ctx, const float* qkv, int d, float* kh, float* vh, int max_len,
+             const int32_t* pos_dev, int rows, int T);
+int lens_from_pos(aur_ctx* ctx, const int32_t* pos, int32_t* lens, int B);
+int advance_pos(aur_ctx* ctx, int32_t* pos, int B);
+int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out);
+// dst[r] = src[(r*row_step + row_off) * ld_src .. + d]
+int gather_rows(aur_ctx* ctx, const float* src, int ld_src, int row_step, int row_off, float* dst,
+                int rows, int d);
+
+// Batched KV decode attention with q rows of stride ld_q (kv_decode.hip).
+int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_history,
+                   const float* v_history, float* out, float* scratch, const int32_t* t_total, int t_max,
+                   int b, int n_head, int d_head, int max_len);
+
+}  // namespace aur

@@ -1,0 +1,181 @@
+"""Python face of the model-level C ABI (aur_model_*, aur_kv_cache_*):
+DecoderTransformerGpu and KvCacheGpu, with the reference's method names
+(src/gpu/transformer.rs, src/gpu/kv_cache.rs).  Every call runs on the
+device through libaurora_hip.so."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from .gpu import GpuContext
+
+LAYER_TENSORS = ("ln1_g", "ln1_b", "w_q", "w_k", "w_v", "w_o", "ln2_g", "ln2_b", "w_fc", "w_proj")
+GLOBAL_TENSORS = ("w_tok", "w_pos", "lnf_g", "lnf_b")
+
+
+class ModelConfig(C.Structure):
+    """aur_model_config (TransformerConfig, src/transformer/model.rs:24-127)."""
+    _fields_ = [("vocab", C.c_uint32), ("d_model", C.c_uint32), ("n_layer", C.c_uint32),
+                ("n_head", C.c_uint32), ("d_ff", C.c_uint32), ("seq_len_max", C.c_uint32)]
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+class DecoderTransformerGpu:
+    def __init__(self, ctx: GpuContext, vocab, d_model, n_layer, n_head, d_ff, seq_len_max,
+                 max_batch: int):
+        self.ctx = ctx
+        self.cfg = ModelConfig(vocab, d_model, n_layer, n_head, d_ff, seq_len_max)
+        out = C.c_void_p()
+        ctx.call("aur_model_create", C.byref(self.cfg), max_batch, C.byref(out))
+        self.ptr = out.value
+        self.max_batch = max_batch
+
+    def _call(self, name, *args):
+        lib = _lib.load()
+        rc = getattr(lib, name)(self.ptr, *args)
+        if rc != 0:
+            raise _lib.AuroraError(name, rc, lib.aur_last_error(self.ctx.ptr).decode())
+
+    def tensor_ptr(self, name: str, layer: int = -1, grad: bool = False) -> tuple[int, int]:
+        p, n = C.c_void_p(), C.c_size_t()
+        self._call("aur_model_tensor", name.encode(), layer, 1 if grad else 0, C.byref(p), C.byref(n))
+        return p.value, n.value
+
+    def get(self, name: str, layer: int = -1, grad: bool = False) -> np.ndarray:
+        p, n = self.tensor_ptr(name, layer, grad)
+        out = np.empty(n, np.float32)
+        self.ctx.call("aur_d2h", out.ctypes.data, p, out.nbytes)
+        return out
+
+    def set(self, name: str, data, layer: int = -1) -> None:
+        p, n = self.tensor_ptr(name, layer)
+        arr = np.ascontiguousarray(data, dtype=np.float32).ravel()
+        if arr.size != n:
+            raise ValueError(f"{name}[{layer}]: {arr.size} values for a tensor of {n}")
+        self.ctx.call("aur_h2d", p, arr.ctypes.data, arr.nbytes)
+
+    def load_params(self, P: dict) -> None:
+        """Upload a parameter dict (oracle.model layout)."""
+        for k in GLOBAL_TENSORS:
+            self.set(k, P[k])
+        for l, L in enumerate(P["layers"]):
+            for k in LAYER_TENSORS:
+                self.set(k, L[k], l)
+
+    def read_tensors(self, grad: bool) -> dict:
+        """Parameters (grad=False) or gradients (grad=True) in the same dict layout."""
+        P = {k: self.get(k, -1, grad) for k in GLOBAL_TENSORS}
+        P["layers"] = [{k: self.get(k, l, grad) for k in LAYER_TENSORS}
+                       for l in range(self.cfg.n_layer)]
+        return P
+
+    def zero_grad(self) -> None:
+        self._call("aur_model_zero_grad")
+
+    def train_step_batch(self, tokens, targets) -> float:
+        tok, tgt = _u32(tokens), _u32(targets)
+        b, t = tok.shape
+        loss = C.c_float()
+        self._call("aur_model_train_step_batch", tok.ctypes.data, tgt.ctypes.data, b, t, C.byref(loss))
+        return loss.value
+
+    def forward(self, tokens, want_logits: bool = True):
+        tok = _u32(tokens)
+        b, t = tok.shape
+        out = np.empty((b * t, self.cfg.vocab), np.float32) if want_logits else None
+        self._call("aur_model_forward", tok.ctypes.data, b, t, out.ctypes.data if want_logits else None)
+        return out
+
+    def clip_grads(self, max_norm: float) -> float:
+        n = C.c_float()
+        self._call("aur_model_clip_grads", max_norm, C.byref(n))
+        return n.value
+
+    def step_adamw(self, lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1) -> None:
+        self._call("aur_model_step_adamw", lr, beta1, beta2, eps, weight_decay)
+
+    def clip_step_adamw(self, max_norm, lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8,
+                        weight_decay=0.1) -> float:
+        n = C.c_float()
+        self._call("aur_model_clip_step_adamw", max_norm, lr, beta1, beta2, eps, weight_decay,
+                   C.byref(n))
+        return n.value
+
+    # KV decode
+    def kv_cache(self, batch: int, max_len: int) -> "KvCacheGpu":
+        return KvCacheGpu(self, batch, max_len)
+
+    def prefill_kv(self, cache: "KvCacheGpu", tokens) -> np.ndarray:
+        tok = _u32(tokens)
+        b, t = tok.shape
+        out = np.empty((b, self.cfg.vocab), np.float32)
+        self._call("aur_model_prefill_kv", cache.ptr, tok.ctypes.data, b, t, out.ctypes.data)
+        return out
+
+    def generate_step_kv(self, cache: "KvCacheGpu", tokens=None, want_logits=True):
+        """One decode step for every sequence; tokens=None feeds the previous argmax.
+        Returns (logits [b, V] or None, argmax tokens [b])."""
+        b = cache.batch
+        tok = _u32(tokens) if tokens is not None else None
+        logits = np.empty((b, self.cfg.vocab), np.float32) if want_logits else None
+        nxt = np.empty(b, np.uint32)
+        self._call("aur_model_generate_step", cache.ptr, tok.ctypes.data if tok is not None else None,
+                   logits.ctypes.data if want_logits else None, nxt.ctypes.data)
+        return logits, nxt
+
+    def generate_greedy(self, cache: "KvCacheGpu", n_steps: int, collect: bool = True):
+        out = np.empty((n_steps, cache.batch), np.uint32) if collect else None
+        self._call("aur_model_generate_greedy", cache.ptr, n_steps,
+                   out.ctypes.data if collect else None)
+        return out
+
+    def destroy(self) -> None:
+        if self.ptr:
+            _lib.load().aur_model_destroy(self.ptr)
+            self.ptr = None
+
+
+class KvCacheGpu:
+    def __init__(self, model: DecoderTransformerGpu, batch: int, max_len: int):
+        self.model = model
+        self.batch = batch
+        self.max_len = max_len
+        out = C.c_void_p()
+        model._call("aur_kv_cache_create", batch, max_len, C.byref(out))
+        self.ptr = out.value
+
+    @property
+    def current_len(self) -> int:
+        n = C.c_uint32()
+        rc = _lib.load().aur_kv_cache_len(self.ptr, C.byref(n))
+        if rc:
+            raise _lib.AuroraError("aur_kv_cache_len", rc, "")
+        return n.value
+
+    def reset(self) -> None:
+        rc = _lib.load().aur_kv_cache_reset(self.ptr)
+        if rc:
+            raise _lib.AuroraError("aur_kv_cache_reset", rc, "")
+
+    def history(self, layer: int) -> tuple[np.ndarray, np.ndarray]:
+        k, v = C.c_void_p(), C.c_void_p()
+        rc = _lib.load().aur_kv_cache_history(self.ptr, layer, C.byref(k), C.byref(v))
+        if rc:
+            raise _lib.AuroraError("aur_kv_cache_history", rc, "")
+        n = self.batch * self.max_len * self.model.cfg.d_model
+        out = []
+        for p in (k.value, v.value):
+            a = np.empty(n, np.float32)
+            self.model.ctx.call("aur_d2h", a.ctypes.data, p, a.nbytes)
+            out.append(a.reshape(self.batch, self.max_len, -1))
+        return out[0], out[1]
+
+    def destroy(self) -> None:
+        if self.ptr:
+            _lib.load().aur_kv_cache_destroy(self.ptr)
+            self.ptr = None

@@ -79,6 +79,140 @@ def time_region(ctx, fn, steps: int) -> float:
     return ms
 
 
+C3 = dict(vocab=8192, d_model=1024, n_layer=12, n_head=16, d_ff=4096, seq_len_max=1024)
+
+
+def init_c3_model(ctx, max_batch, seed):
+    """BASELINE config-3 model: every weight N(0,0.02), W_o and W_proj ×
+    1/sqrt(2·12), LN γ = 1, β = 0 (random init, no checkpoint)."""
+    from aurora_amd.model import DecoderTransformerGpu
+
+    m = DecoderTransformerGpu(ctx, max_batch=max_batch, **C3)
+    rng = np.random.default_rng(seed)
+    n = m.tensor_ptr("params")[1]
+    m.set("params", rng.standard_normal(n, dtype=np.float32) * np.float32(0.02))
+    d, L = C3["d_model"], C3["n_layer"]
+    res = np.float32(1.0 / np.sqrt(2.0 * L))
+    for l in range(L):
+        m.set("w_o", m.get("w_o", l) * res, l)
+        m.set("w_proj", m.get("w_proj", l) * res, l)
+        for k in ("ln1_g", "ln2_g"):
+            m.set(k, np.ones(d, np.float32), l)
+        for k in ("ln1_b", "ln2_b"):
+            m.set(k, np.zeros(d, np.float32), l)
+    m.set("lnf_g", np.ones(d, np.float32))
+    m.set("lnf_b", np.zeros(d, np.float32))
+    return m
+
+
+def c3_step_flops(B=16, T=1024) -> float:
+    """Algorithmic FLOP of one config-3 training step: 6·tokens·(linear + head
+    params) for the GEMMs plus causal attention (4·dh per causal pair forward,
+    10·dh backward) — 17.11 TFLOP at B16 T1024."""
+    d, L, F, V, H = C3["d_model"], C3["n_layer"], C3["d_ff"], C3["vocab"], C3["n_head"]
+    tokens = B * T
+    lin = L * (4 * d * d + 2 * d * F) + V * d
+    pairs = B * H * T * (T + 1) / 2
+    return 6.0 * tokens * lin + L * 14.0 * (d // H) * pairs
+
+
+def bench_train(ctx, steps: int, warmup: int) -> dict:
+    """Config 3: one full training step (forward, CE, backward, clip 1.0,
+    AdamW lr 3e-4 wd 0.1) on B16 × T1024 synthetic tokens, timed with events."""
+    B, T = 16, 1024
+    m = init_c3_model(ctx, B, seed=2)
+    rng = np.random.default_rng(2)
+    seq = rng.integers(0, C3["vocab"], (B, T + 1)).astype(np.uint32)
+    tok, tgt = seq[:, :T].copy(), seq[:, 1:].copy()
+
+    losses = []
+
+    def step():
+        m.zero_grad()
+        losses.append(m.train_step_batch(tok, tgt) / B)
+        m.clip_step_adamw(1.0, lr=3e-4, weight_decay=0.1)
+
+    for _ in range(warmup):
+        step()
+    ms = time_region(ctx, step, steps)
+    m.destroy()
+    tok_s = B * T / (ms * 1e-3)
+    tf = c3_step_flops(B, T) / (ms * 1e-3) / 1e12
+    log(f"[bench] train C3: {ms:.2f} ms/step {tok_s:.0f} tok/s {tf:.1f} TFLOP/s "
+        f"loss {losses[0]:.4f} -> {losses[-1]:.4f}")
+    return {"ms_per_step": round(ms, 3), "tok_per_s": round(tok_s, 1), "tflops": round(tf, 2),
+            "pct_peak": round(100 * tf / PEAK_FP32_MFMA, 1), "loss_first": round(losses[0], 5),
+            "loss_last": round(losses[-1], 5), "steps": steps,
+            "config": "V8192 d1024 L12 H16 d_ff4096 T1024 B16 fp32, clip 1.0, AdamW lr 3e-4 wd 0.1"}
+
+
+def bench_decode(ctx, n_steps: int = 256) -> dict:
+    """Config 4: prefill 32 prompts × 512 tokens, then n_steps greedy
+    generate_step calls for all 32 sequences (KV ≤ 768), device-resident."""
+    B, T0 = 32, 512
+    max_len = T0 + n_steps
+    m = init_c3_model(ctx, B, seed=2)
+    rng = np.random.default_rng(4)
+    prompts = rng.integers(0, C3["vocab"], (B, T0)).astype(np.uint32)
+    cache = m.kv_cache(B, max_len)
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record()
+    m.prefill_kv(cache, prompts)
+    e1.record()
+    prefill_ms = e0.elapsed_ms(e1)
+    # warm the decode path on a scratch cache, then time the real run
+    ctx.sync()
+    e0.record()
+    m.generate_greedy(cache, n_steps, collect=False)
+    e1.record()
+    ms = e0.elapsed_ms(e1)
+    d, L, F, V = C3["d_model"], C3["n_layer"], C3["d_ff"], C3["vocab"]
+    w_bytes = 4.0 * (L * (4 * d * d + 2 * d * F + 4 * d) + V * d + 2 * d + B * d)
+    kv_read = sum(4.0 * 2 * L * B * (T0 + s + 1) * d for s in range(n_steps))
+    kv_write = 4.0 * 2 * L * B * d * n_steps
+    logits = 4.0 * B * V * n_steps
+    total = w_bytes * n_steps + kv_read + kv_write + logits
+    gbs = total / (ms * 1e-3) / 1e9
+    tok_s = B * n_steps / (ms * 1e-3)
+    cache.destroy()
+    m.destroy()
+    log(f"[bench] decode C4: prefill {prefill_ms:.2f} ms, {n_steps} steps {ms:.2f} ms "
+        f"({ms / n_steps:.3f} ms/step) {tok_s:.0f} tok/s {gbs:.0f} GB/s")
+    return {"prefill_ms": round(prefill_ms, 3), "ms_per_step": round(ms / n_steps, 4),
+            "tok_per_s": round(tok_s, 1), "gb_per_s": round(gbs, 1),
+            "pct_hbm": round(100 * gbs / PEAK_HBM, 1), "bytes_per_step": round(total / n_steps),
+            "config": f"C3 model, {B} prompts x {T0} tokens prefill, {n_steps} greedy steps, KV<= {max_len}"}
+
+
+def bench_attention(ctx, steps: int) -> dict:
+    """Config 2: causal MHA forward + 3-pass backward, B16 H8 T1024 dh64."""
+    from aurora_amd.gpu import CausalMhaBackwardKernel, CausalMhaForwardKernel, GpuBuffer
+
+    B, T, H, dh = 16, 1024, 8, 64
+    n = B * T * H * dh
+    rng = np.random.default_rng(1)
+    q, k, v, do = (GpuBuffer.from_slice(ctx, rng.standard_normal(n, dtype=np.float32)) for _ in range(4))
+    o, lse = GpuBuffer.empty(ctx, n), GpuBuffer.empty(ctx, B * H * T)
+    dq, dk, dv = (GpuBuffer.zeros(ctx, n) for _ in range(3))
+    ws = GpuBuffer.empty(ctx, CausalMhaBackwardKernel.workspace_len(T, H, B))
+    fwd, bwd = CausalMhaForwardKernel(), CausalMhaBackwardKernel()
+    f = lambda: fwd.dispatch_into(ctx, q, k, v, o, lse, T, H, dh, b=B)
+    g = lambda: bwd.dispatch_into(ctx, q, k, v, o, lse, do, dq, dk, dv, ws, T, H, dh, b=B)
+    f()
+    g()
+    ms_f = time_region(ctx, f, steps)
+    ms_b = time_region(ctx, g, steps)
+    pairs = B * H * T * (T + 1) / 2
+    tf_f = 4.0 * dh * pairs / (ms_f * 1e-3) / 1e12
+    tf_b = 10.0 * dh * pairs / (ms_b * 1e-3) / 1e12
+    for x in (q, k, v, do, o, lse, dq, dk, dv, ws):
+        x.free()
+    log(f"[bench] attention C2: fwd {ms_f:.3f} ms {tf_f:.1f} TFLOP/s, bwd {ms_b:.3f} ms {tf_b:.1f} TFLOP/s")
+    return {"fwd_ms": round(ms_f, 4), "fwd_tflops": round(tf_f, 2), "bwd_ms": round(ms_b, 4),
+            "bwd_tflops": round(tf_b, 2), "config": "B16 H8 T1024 dh64 causal fp32"}
+
+
 def cpu_baseline(budget_s: float = 10.0) -> dict:
     """The reference CPU path's GEMM: linear_forward (src/attention.rs:219-238)
     restated in oracle/, one 64-row "sequence" per task over a thread pool as
@@ -111,8 +245,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["head", "sweep"], default=None,
+    ap.add_argument("--only", choices=["head", "sweep", "train", "decode", "attention"], default=None,
                     help="profile helper: time only this part and skip the CPU baseline")
+    ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -135,6 +270,15 @@ def main() -> int:
             head[2]()
         ms = time_region(ctx, head[2], args.steps)
         log(f"[bench] head gemm {ms:.4f} ms  {head[1] / ms / 1e9:.1f} TFLOP/s")
+        return 0
+    if args.only == "train":
+        bench_train(ctx, max(1, args.steps), args.warmup)
+        return 0
+    if args.only == "decode":
+        bench_decode(ctx, args.decode_steps)
+        return 0
+    if args.only == "attention":
+        bench_attention(ctx, args.steps)
         return 0
 
     def step():
@@ -163,6 +307,9 @@ def main() -> int:
 
     if args.only == "sweep":
         return 0
+    attn = bench_attention(ctx, max(3, args.steps // 4))
+    train = bench_train(ctx, max(2, min(args.steps, 5)), min(args.warmup, 2))
+    decode = bench_decode(ctx, args.decode_steps)
     cpu = cpu_baseline(args.cpu_budget)
     log(f"[bench] cpu baseline {cpu}")
 
@@ -185,6 +332,9 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "pct_peak": round(100 * value / PEAK_FP32_MFMA, 2),
         "sweep": per,
+        "attention": attn,
+        "train": train,
+        "decode": decode,
         "roofline": {"bound": "mfma", "kernel": "gemm_f32_mfma (tied head, NT 8192x8192x512)",
                      "achieved": round(head_tf, 3), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(head_tf / PEAK_FP32_MFMA, 4), "traffic": None},

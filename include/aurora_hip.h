@@ -173,6 +173,74 @@ int aur_mha_kv_step_batched(aur_ctx* ctx, const float* q_new,
                             uint32_t t_max, uint32_t b, uint32_t n_head,
                             uint32_t d_head, uint32_t max_len);
 
+/* ---- model: DecoderTransformerGpu / KvCacheGpu ----------------------------
+ * The caller of the hot path (src/gpu/transformer.rs:32-116, 949-2640),
+ * running B sequences through every GEMM together (M = B·T rows).  The
+ * pre-LN GPT of the reference with optional features off: tied head, learned
+ * positions, LayerNorm eps 1e-5, tanh-GELU FFN. */
+typedef struct aur_model aur_model;
+typedef struct aur_kv_cache aur_kv_cache;
+typedef struct {
+  uint32_t vocab, d_model, n_layer, n_head, d_ff, seq_len_max;
+} aur_model_config; /* TransformerConfig, src/transformer/model.rs:24-127 */
+
+/* DecoderTransformerGpu::from_cpu (transformer.rs:949) without the upload:
+ * allocates parameters (zero), gradients, AdamW moments and the activation
+ * arena for max_batch × seq_len_max rows.  Parameters are then written
+ * through aur_model_tensor pointers. */
+int aur_model_create(aur_ctx* ctx, const aur_model_config* cfg, uint32_t max_batch, aur_model** out);
+int aur_model_destroy(aur_model* m);
+/* Device pointer + length of a parameter (grad = 0) or its gradient
+ * (grad = 1): "w_tok", "w_pos", "lnf_g", "lnf_b", and per layer "ln1_g",
+ * "ln1_b", "w_q", "w_k", "w_v" (rows of "w_qkv" = [w_q; w_k; w_v]), "w_o",
+ * "ln2_g", "ln2_b", "w_fc", "w_proj"; "params" / "grads" are the flat
+ * buffers.  Replaces the public field p: GpuParams (transformer.rs:86). */
+int aur_model_tensor(aur_model* m, const char* name, int32_t layer, int32_t grad, float** ptr,
+                     size_t* len);
+/* zero_grad (transformer.rs:1242). */
+int aur_model_zero_grad(aur_model* m);
+/* train_step_batch (transformer.rs:1571): forward + softmax-CE + backward for
+ * b host sequences of length t (tokens/targets [b*t]); gradients accumulate
+ * as the batch MEAN of per-sequence mean-over-t losses (the CPU trainer's
+ * convention, examples/aurora_train.rs:840-846).  *loss_sum = Σ_b mean_t NLL. */
+int aur_model_train_step_batch(aur_model* m, const uint32_t* tokens, const uint32_t* targets,
+                               uint32_t b, uint32_t t, float* loss_sum);
+/* Forward only (encode_forward, transformer.rs:1347); logits [b*t, vocab]
+ * copied to the host buffer `logits` when non-NULL. */
+int aur_model_forward(aur_model* m, const uint32_t* tokens, uint32_t b, uint32_t t, float* logits);
+/* clip_grads (model.rs:1011-1017): global L2 over all gradients, scaled in
+ * place when above max_norm; *norm = the pre-clip norm. */
+int aur_model_clip_grads(aur_model* m, float max_norm, float* norm);
+/* step_adamw (model.rs:926-1009, transformer.rs:2008). */
+int aur_model_step_adamw(aur_model* m, float lr, float beta1, float beta2, float eps,
+                         float weight_decay);
+/* clip_grads + step_adamw fused (the clip factor is applied inside AdamW). */
+int aur_model_clip_step_adamw(aur_model* m, float max_norm, float lr, float beta1, float beta2,
+                              float eps, float weight_decay, float* norm);
+
+/* KvCacheGpu::new (kv_cache.rs:42) for `batch` sequences decoded together,
+ * max_len <= seq_len_max; reset zeroes it (kv_cache.rs:76). */
+int aur_kv_cache_create(aur_model* m, uint32_t batch, uint32_t max_len, aur_kv_cache** out);
+int aur_kv_cache_reset(aur_kv_cache* c);
+int aur_kv_cache_destroy(aur_kv_cache* c);
+int aur_kv_cache_len(aur_kv_cache* c, uint32_t* len);
+/* Device K / V history of `layer`, each [batch, max_len, d_model]. */
+int aur_kv_cache_history(aur_kv_cache* c, uint32_t layer, float** k, float** v);
+/* prefill_kv (transformer.rs:2374; CPU KvCache::prefill kv_cache.rs:70):
+ * full forward of b prompts of length t filling the cache; last-position
+ * logits [b, vocab] to the host when non-NULL; the cache's next input
+ * tokens become their argmax (the first greedy token). */
+int aur_model_prefill_kv(aur_model* m, aur_kv_cache* c, const uint32_t* tokens, uint32_t b,
+                         uint32_t t, float* last_logits);
+/* generate_step_kv (transformer.rs:2410; CPU generate_step kv_cache.rs:97)
+ * for all b sequences: `tokens` [b] from the host, or NULL to feed the
+ * previous step's argmax (greedy, no host round trip).  Logits [b, vocab]
+ * and the argmax tokens [b] are copied out when the pointers are non-NULL. */
+int aur_model_generate_step(aur_model* m, aur_kv_cache* c, const uint32_t* tokens, float* logits,
+                            uint32_t* next_tokens);
+/* n_steps greedy generate_step calls; out_tokens [n_steps, b] or NULL. */
+int aur_model_generate_greedy(aur_model* m, aur_kv_cache* c, uint32_t n_steps, uint32_t* out_tokens);
+
 #ifdef __cplusplus
 }
 #endif

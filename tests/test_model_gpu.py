@@ -1,0 +1,224 @@
+"""GPU parity of the model level: DecoderTransformerGpu train step at
+M = B·T and the batched KV-cache decode, through the C ABI.
+
+Mirrors tests/gpu_parity.rs:569-1148 (loss |Δ| < 5e-2, grads < 5e-2,
+train_step_loss_matches_cpu_baseline 5e-3, batch == Σ sequential) and
+tests/kv_cache.rs (GPU KV vs CPU KV 5e-2 :232-279, greedy identity
+:166-213 / :283-329, t_total > 64 stride loops :346-386), with the CPU
+oracle (oracle.model) as the reference CPU path.
+"""
+import numpy as np
+import pytest
+
+from oracle import model as OM
+from tests.parity import fro_rel
+
+pytestmark = pytest.mark.gpu
+
+# V256 d128 L2 H4 d_ff512 T64 B8, seed 0.
+C0 = OM.Config(vocab=256, d_model=128, n_layer=2, n_head=4, d_ff=512, seq_len_max=64)
+
+
+def _gpu_model(ctx, cfg, max_batch, P):
+    from aurora_amd.model import DecoderTransformerGpu
+
+    m = DecoderTransformerGpu(ctx, cfg.vocab, cfg.d_model, cfg.n_layer, cfg.n_head, cfg.d_ff,
+                              cfg.seq_len_max, max_batch)
+    m.load_params(P)
+    return m
+
+
+def _tokens(cfg, B, T, seed):
+    rng = np.random.default_rng(seed)
+    seq = rng.integers(0, cfg.vocab, (B, T + 1)).astype(np.uint32)
+    return seq[:, :T].copy(), seq[:, 1:].copy()
+
+
+def _compare_tree(got, want, tol, what):
+    worst = 0.0
+    for (name, l, g), (_, _, w) in zip(OM.tensors(got), OM.tensors(want)):
+        e = fro_rel(g, w)
+        worst = max(worst, e)
+        assert e < tol, (what, name, l, e)
+    return worst
+
+
+def test_config0_train_step_matches_cpu(ctx):
+    """One forward + backward + clip(1.0) + AdamW(lr 3e-4, wd 0.1) step."""
+    cfg = C0
+    P = OM.init_params(cfg, 0)
+    tok, tgt = _tokens(cfg, 8, 64, 0)
+    m = _gpu_model(ctx, cfg, 8, P)
+    m.zero_grad()
+    loss_gpu = m.train_step_batch(tok, tgt)
+    G_gpu = m.read_tensors(grad=True)
+
+    loss_cpu, G = OM.batch_grads(P, cfg, tok, tgt)
+    assert abs(loss_gpu - loss_cpu) < 5e-3 * 8, (loss_gpu, loss_cpu)  # Σ over 8 sequence means
+    worst_g = _compare_tree(G_gpu, G, 1e-3, "grad")
+
+    norm_gpu = m.clip_grads(1.0)
+    m.step_adamw(lr=3e-4, weight_decay=0.1)
+    norm_cpu = OM.clip_grads(G, 1.0)
+    st = OM.new_adam_state(P)
+    OM.step_adamw(P, G, st, lr=3e-4, wd=0.1)
+    assert abs(norm_gpu - norm_cpu) < 1e-4 * max(1.0, norm_cpu), (norm_gpu, norm_cpu)
+    worst_p = _compare_tree(m.read_tensors(grad=False), P, 1e-5, "param")
+    print(f"[config0] loss gpu {loss_gpu:.6f} cpu {loss_cpu:.6f} |grad err| <= {worst_g:.2e} "
+          f"norm {norm_gpu:.5f}/{norm_cpu:.5f} |param err| <= {worst_p:.2e}")
+    m.destroy()
+
+
+def test_fused_clip_adamw_equals_separate(ctx):
+    cfg = C0
+    P = OM.init_params(cfg, 1)
+    tok, tgt = _tokens(cfg, 4, 64, 1)
+    outs = []
+    for fused in (False, True):
+        m = _gpu_model(ctx, cfg, 4, P)
+        m.zero_grad()
+        m.train_step_batch(tok, tgt)
+        if fused:
+            m.clip_step_adamw(0.05, lr=3e-4, weight_decay=0.1)
+        else:
+            m.clip_grads(0.05)
+            m.step_adamw(lr=3e-4, weight_decay=0.1)
+        outs.append(m.get("params"))
+        m.destroy()
+    np.testing.assert_allclose(outs[0], outs[1], rtol=0, atol=1e-7)
+
+
+def test_train_step_deterministic_and_batch_additive(ctx):
+    cfg = C0
+    P = OM.init_params(cfg, 2)
+    tok, tgt = _tokens(cfg, 4, 64, 2)
+    m = _gpu_model(ctx, cfg, 4, P)
+    m.zero_grad()
+    m.train_step_batch(tok, tgt)
+    g1 = m.get("grads")
+    m.zero_grad()
+    m.train_step_batch(tok, tgt)
+    g2 = m.get("grads")
+    assert np.array_equal(g1, g2)  # bitwise run to run (no atomics anywhere)
+    # batch of 4 == mean of two batches of 2 (stability.rs:167 additivity)
+    m.zero_grad()
+    m.train_step_batch(tok[:2], tgt[:2])
+    ga = m.get("grads")
+    m.zero_grad()
+    m.train_step_batch(tok[2:], tgt[2:])
+    gb = m.get("grads")
+    assert fro_rel(g1, (ga + gb) / 2) < 1e-5
+    m.destroy()
+
+
+def test_ragged_seq_lengths_forward_matches_cpu(ctx):
+    cfg = OM.Config(vocab=64, d_model=64, n_layer=2, n_head=4, d_ff=128, seq_len_max=100)
+    P = OM.init_params(cfg, 5)
+    m = _gpu_model(ctx, cfg, 3, P)
+    for T in (1, 17, 65, 100):
+        tok, _ = _tokens(cfg, 3, T, T)
+        got = m.forward(tok)
+        for b in range(3):
+            want, _ = OM.forward(P, cfg, tok[b])
+            assert fro_rel(got[b * T:(b + 1) * T], want) < 1e-4, (T, b)
+    m.destroy()
+
+
+# ------------------------------------------------------------------ decode
+def test_kv_decode_matches_cpu_generate_step(ctx):
+    """kv_cache.rs:232-279 at d_head 32, prompts 70 > 64 (stride loops)."""
+    cfg = OM.Config(vocab=96, d_model=128, n_layer=2, n_head=4, d_ff=256, seq_len_max=96)
+    P = OM.init_params(cfg, 9)
+    B, T0, steps = 3, 70, 10
+    rng = np.random.default_rng(9)
+    prompts = rng.integers(0, cfg.vocab, (B, T0)).astype(np.uint32)
+    feed = rng.integers(0, cfg.vocab, (steps, B)).astype(np.uint32)
+    m = _gpu_model(ctx, cfg, B, P)
+    cache = m.kv_cache(B, cfg.seq_len_max)
+    last = m.prefill_kv(cache, prompts)
+    cpu = [OM.KvCache(cfg) for _ in range(B)]
+    for b in range(B):
+        full = cpu[b].prefill(P, prompts[b])
+        assert fro_rel(last[b], full.reshape(T0, -1)[-1]) < 1e-4
+    for s in range(steps):
+        logits, _ = m.generate_step_kv(cache, feed[s])
+        for b in range(B):
+            want = OM.generate_step(P, cfg, cpu[b], int(feed[s, b]))
+            assert fro_rel(logits[b], want) < 1e-4, (s, b)
+    assert cache.current_len == T0 + steps
+    # the cached K/V rows equal the CPU cache's
+    k0, v0 = cache.history(0)
+    assert fro_rel(k0[1, :T0 + steps], cpu[1].k[0].reshape(T0 + steps, -1)) < 1e-4
+    cache.destroy()
+    m.destroy()
+
+
+def test_greedy_kv_decode_token_identical_to_full_forward(ctx):
+    """kv_cache.rs:166-213 / :283-329: greedy tokens from the KV path equal the
+    greedy tokens of a full forward over the growing sequence."""
+    cfg = OM.Config(vocab=128, d_model=128, n_layer=2, n_head=2, d_ff=256, seq_len_max=64)
+    P = OM.init_params(cfg, 13)
+    B, T0, steps = 4, 20, 24
+    rng = np.random.default_rng(13)
+    prompts = rng.integers(0, cfg.vocab, (B, T0)).astype(np.uint32)
+    m = _gpu_model(ctx, cfg, B, P)
+    cache = m.kv_cache(B, cfg.seq_len_max)
+    last = m.prefill_kv(cache, prompts)
+    first = last.argmax(1).astype(np.uint32)
+    toks = m.generate_greedy(cache, steps)  # toks[s] = argmax after feeding step s's token
+    kv_seq = np.concatenate([prompts, first[:, None], toks.T], axis=1)  # T0 + 1 + steps
+    # full-forward greedy on the same growing sequences (one batch forward per step)
+    seq = np.concatenate([prompts, first[:, None]], axis=1)
+    for s in range(steps):
+        logits = m.forward(seq).reshape(B, seq.shape[1], -1)[:, -1]
+        nxt = logits.argmax(1).astype(np.uint32)
+        order = np.sort(logits, axis=1)
+        gap = order[:, -1] - order[:, -2]
+        assert np.array_equal(nxt, kv_seq[:, T0 + 1 + s]), (s, nxt, kv_seq[:, T0 + 1 + s], gap)
+        seq = np.concatenate([seq, nxt[:, None]], axis=1)
+    # and against the CPU oracle's greedy decode for one sequence
+    kv = OM.KvCache(cfg)
+    lg = kv.prefill(P, prompts[0])
+    tok = OM.argmax(lg.reshape(T0, -1)[-1])
+    cpu_seq = [tok]
+    for _ in range(steps):
+        lg = OM.generate_step(P, cfg, kv, tok)
+        tok = OM.argmax(lg)
+        cpu_seq.append(tok)
+    assert cpu_seq == list(kv_seq[0, T0:]), (cpu_seq, kv_seq[0, T0:])
+    cache.destroy()
+    m.destroy()
+
+
+# -------------------------------------------------------- BASELINE shapes
+def test_config3_shape_train_step_runs(ctx):
+    """Full config-3 shapes (V8192 d1024 L12 H16 d_ff4096 T1024 B16): loss at
+    init ≈ ln V, finite grads, bitwise repeatable.  The CPU oracle would take
+    minutes here; the parity gates at this scale are these properties."""
+    cfg = OM.Config(vocab=8192, d_model=1024, n_layer=12, n_head=16, d_ff=4096, seq_len_max=1024)
+    from aurora_amd.model import DecoderTransformerGpu
+
+    m = DecoderTransformerGpu(ctx, cfg.vocab, cfg.d_model, cfg.n_layer, cfg.n_head, cfg.d_ff,
+                              cfg.seq_len_max, 16)
+    rng = np.random.default_rng(2)
+    flat = (rng.standard_normal(m.tensor_ptr("params")[1], dtype=np.float32) * np.float32(0.02))
+    m.set("params", flat)
+    for l in range(cfg.n_layer):
+        for k in ("ln1_g", "ln2_g"):
+            m.set(k, np.ones(cfg.d_model, np.float32), l)
+        for k in ("ln1_b", "ln2_b"):
+            m.set(k, np.zeros(cfg.d_model, np.float32), l)
+    m.set("lnf_g", np.ones(cfg.d_model, np.float32))
+    m.set("lnf_b", np.zeros(cfg.d_model, np.float32))
+    tok, tgt = _tokens(cfg, 16, 1024, 2)
+    m.zero_grad()
+    loss = m.train_step_batch(tok, tgt) / 16
+    g1 = m.get("grads")
+    assert abs(loss - np.log(8192)) < 0.5, loss
+    assert np.all(np.isfinite(g1))
+    m.zero_grad()
+    m.train_step_batch(tok, tgt)
+    assert np.array_equal(g1, m.get("grads"))
+    norm = m.clip_step_adamw(1.0, lr=3e-4, weight_decay=0.1)
+    assert np.isfinite(norm) and norm > 0
+    m.destroy()
