@@ -220,6 +220,7 @@ class DecoderTransformerGpu {
   struct Layer;
   struct Acts;
   void encode_forward(uint32_t b, uint32_t t, KvCacheGpu* cache, bool head_all_rows);
+  void encode_decode_step(KvCacheGpu& cache);
   void encode_backward(uint32_t b, uint32_t t);
   void upload_tokens(const uint32_t* tokens, const uint32_t* targets, uint32_t b, uint32_t t);
 
@@ -259,7 +260,10 @@ class KvCacheGpu {
   uint32_t* tok_ = nullptr;
   float *x_ = nullptr, *ln_ = nullptr, *qkv_ = nullptr, *attn_ = nullptr, *xmid_ = nullptr;
   float *hpre_ = nullptr, *hpost_ = nullptr, *logits_ = nullptr, *scratch_ = nullptr;
+  float* part_ = nullptr;  // K-range partial products of the W_o / W_proj decode GEMMs
+  size_t part_floats_ = 0;
   size_t bytes_ = 0;
+  void* graph_ = nullptr;       // hipGraphExec_t of one decode step, built on first use
 };
 
 }  // namespace aurora

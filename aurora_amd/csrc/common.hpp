@@ -46,12 +46,24 @@ struct Epilogue {
   float* C2 = nullptr;
 };
 
+// Caller-owned scratch for split-K partial tiles (used instead of the
+// context's grow-only workspace, e.g. by work captured into a HIP graph).
+struct Workspace {
+  float* ptr = nullptr;
+  size_t floats = 0;
+};
+
 // C = epilogue(op(A)·op(B)).  a_kcontig: A(m,k) = A[m*lda+k], else A[k*lda+m];
 // b_kcontig: B(k,n) = B[n*ldb+k], else B[k*ldb+n].  Enqueued on ctx's stream.
 int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
-         int ldb, float* C, int ldc, int M, int N, int K, const Epilogue& epi);
+         int ldb, float* C, int ldc, int M, int N, int K, const Epilogue& epi,
+         const Workspace* ws = nullptr);
 int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
          int ldb, float* C, int ldc, int M, int N, int K, bool accumulate);
+// Decode-shaped A@Bᵀ (M ≤ 64) split into `splits` K ranges whose products
+// are stored to P[splits][M][N] for the consumer to sum in range order.
+int gemm_nt_partials(aur_ctx* ctx, const float* A, int lda, const float* B, int ldb, float* P, int M, int N,
+                     int K, int splits);
 
 }  // namespace aur
 

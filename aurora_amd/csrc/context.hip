@@ -43,6 +43,13 @@ int ensure_workspace(aur_ctx* ctx, size_t bytes) {
   if (e != hipSuccess)
     return set_error(ctx, AUR_ENOMEM, "workspace of %zu bytes: %s", want,
                      hipGetErrorString(e));
+  // Zeroed once: the head of the workspace holds arrival counters that every
+  // kernel using them leaves at zero when it finishes.
+  e = hipMemsetAsync(p, 0, want, ctx->stream);
+  if (e != hipSuccess) {
+    hipFree(p);
+    return set_error(ctx, (int)e, "workspace memset: %s", hipGetErrorString(e));
+  }
   ctx->ws = p;
   ctx->ws_bytes = want;
   return 0;

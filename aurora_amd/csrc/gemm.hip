@@ -272,6 +272,83 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ P
   }
 }
 
+// ------------------------------------------------------------ skinny A@Bᵀ
+// Decode-shaped C[M ≤ 16·MT, N] = X[M, K]·W[N, K]ᵀ (M = sequences decoded
+// together): bound by streaming W once, and too small for the tiled
+// kernel's per-K-step LDS pipeline.  A block owns 16 columns of N and ALL
+// of K; its W waves take 1/W of K each, keep U k-chunks of W and X
+// fragments in flight (X, a few hundred KB, comes from L2) and alternate
+// two accumulator sets so the MFMA dependency chains are half as deep; the
+// W partial tiles are summed through LDS in wave order (deterministic)
+// before the epilogue.  One launch, no inter-block sync.  With gridDim.y > 1
+// the block only covers K range blockIdx.y of gridDim.y and stores its tile
+// to P[blockIdx.y] with no epilogue: the CONSUMER of the product sums the
+// ranges in increasing order (the decode step's LayerNorm does, together
+// with the residual add).
+template <int MT, int W>
+__global__ void __launch_bounds__(64 * W) skinny_nt_kernel(GemmArgs g) {
+  constexpr int U = 8;  // 16-wide k-chunks in flight per wave
+  __shared__ float red[W][16 * MT][17];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g16 = lane >> 4, l16 = lane & 15;
+  const int n0 = blockIdx.x * 16;
+  const int n = n0 + l16;
+  const bool nval = n < g.N;
+  const int nchunks_all = (g.K + 15) / 16;
+  const int cpb = (nchunks_all + gridDim.y - 1) / gridDim.y;  // chunks of this block's K range
+  const int kb = blockIdx.y * cpb, nchunks = min(nchunks_all, kb + cpb);
+  const int per = (cpb + W - 1) / W;
+  const int cb = kb + w * per, ce = min(nchunks, cb + per);
+  const float* wrow = g.B + (size_t)(nval ? n : 0) * g.ldb;
+  floatx4 acc[MT], acc2[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = acc2[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = cb; c0 < ce; c0 += U) {
+    floatx4 wf[U], xf[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = 16 * (c0 + u) + 4 * g16;
+      const bool kval = c0 + u < ce && k < g.K;  // K % 4 == 0: a float4 is all in or all out
+      floatx4 v = {0.f, 0.f, 0.f, 0.f};
+      if (nval && kval) v = *reinterpret_cast<const floatx4*>(wrow + k);
+      wf[u] = v;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int r = 16 * i + l16;
+        floatx4 x = {0.f, 0.f, 0.f, 0.f};
+        if (kval && r < g.M) x = *reinterpret_cast<const floatx4*>(g.A + (size_t)r * g.lda + k);
+        xf[u][i] = x;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u += 2)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          acc[i] = mfma16x16x4(xf[u][i][s], wf[u][s], acc[i]);
+          acc2[i] = mfma16x16x4(xf[u + 1][i][s], wf[u + 1][s], acc2[i]);
+        }
+  }
+  // acc + acc2 = partial C[16i + 4·g16 + e][n0 + l16] of this wave's K range
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[w][16 * i + 4 * g16 + e][l16] = acc[i][e] + acc2[i][e];
+  __syncthreads();
+  for (int idx = tid; idx < 16 * MT * 16; idx += 64 * W) {
+    const int row = idx >> 4, col = idx & 15;
+    if (row >= g.M || n0 + col >= g.N) continue;
+    float v = red[0][row][col];
+#pragma unroll
+    for (int ww = 1; ww < W; ++ww) v += red[ww][row][col];
+    if (gridDim.y > 1)
+      g.P[((size_t)blockIdx.y * g.M + row) * g.N + n0 + col] = v;
+    else
+      apply_epilogue(g.epi, g.C, (size_t)row * g.ldc + n0 + col, v);
+  }
+}
+
 struct Plan {
   int bm, bn, splits, k_chunk;
 };
@@ -344,10 +421,51 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 namespace aur {
 
+// Split-K partial tiles: the caller's workspace (ws) or the context's
+// grow-only one.
+static int partials(aur_ctx* ctx, const Workspace* ws, size_t floats, float** out) {
+  if (ws && ws->ptr) {
+    if (ws->floats < floats)
+      return set_error(ctx, AUR_ENOMEM, "gemm: workspace of %zu floats, %zu needed", ws->floats, floats);
+    *out = ws->ptr;
+    return 0;
+  }
+  int rc = ensure_workspace(ctx, floats * sizeof(float));
+  if (rc) return rc;
+  *out = static_cast<float*>(ctx->ws);
+  return 0;
+}
+
+static void reduce_partials(aur_ctx* ctx, const float* P, float* C, int M, int N, int ldc, int splits,
+                            const Epilogue& epi) {
+  const size_t total = (size_t)M * N;
+  int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+  hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, P, C, M, N, ldc, splits, epi);
+}
+
+// Decode-shaped A@Bᵀ (M ≤ 64, both operands k-contiguous, 16-byte vectors).
+// splits > 1: K ranges write P[splits][M][N] instead of C (no epilogue).
+static int skinny_nt(aur_ctx* ctx, const float* A, int lda, const float* B, int ldb, float* C, int ldc,
+                     int M, int N, int K, const Epilogue& epi, float* P = nullptr, int splits = 1) {
+  GemmArgs a{};
+  a.A = A; a.B = B; a.C = C; a.M = M; a.N = N; a.K = K;
+  a.lda = lda; a.ldb = ldb; a.ldc = ldc; a.epi = epi; a.P = P;
+  // 16 waves per block (K split 16 ways) while the registers allow it.
+  dim3 grid((N + 15) / 16, splits);
+  if (M <= 16)
+    hipLaunchKernelGGL((skinny_nt_kernel<1, 16>), grid, dim3(1024), 0, ctx->stream, a);
+  else if (M <= 32)
+    hipLaunchKernelGGL((skinny_nt_kernel<2, 16>), grid, dim3(1024), 0, ctx->stream, a);
+  else
+    hipLaunchKernelGGL((skinny_nt_kernel<4, 8>), grid, dim3(512), 0, ctx->stream, a);
+  AUR_LAUNCH_CHECK(ctx, "skinny_nt_kernel");
+  return 0;
+}
+
 // C = epilogue(op(A)·op(B)) on ctx's stream.  See aur_gemm_ex for operand
 // meaning and Epilogue (common.hpp) for the fused output forms.
 int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
-         int ldb, float* C, int ldc, int M, int N, int K, const Epilogue& epi) {
+         int ldb, float* C, int ldc, int M, int N, int K, const Epilogue& epi, const Workspace* ws) {
   if (M < 0 || N < 0 || K < 0) return set_error(ctx, AUR_EINVAL, "gemm: negative dims");
   if (M == 0 || N == 0) return 0;
   if (!C || (K > 0 && (!A || !B))) return set_error(ctx, AUR_EINVAL, "gemm: null pointer");
@@ -367,6 +485,8 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
   const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                    (a_kcontig ? (K % 4 == 0) : (a_rows % 4 == 0)) &&
                    (b_kcontig ? (K % 4 == 0) : (b_rows % 4 == 0));
+  if (vec && a_kcontig && b_kcontig && M <= 64)
+    return skinny_nt(ctx, A, lda, B, ldb, C, ldc, M, N, K, epi);
   // Split-K only pays for long K with few output tiles; used for every form.
   Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/true);
   GemmArgs a{};
@@ -384,10 +504,8 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
   a.k_chunk = p.k_chunk;
   a.epi = epi;
   if (p.splits > 1) {
-    const size_t need = (size_t)p.splits * M * N * sizeof(float);
-    int rc = ensure_workspace(ctx, need);
+    int rc = partials(ctx, ws, (size_t)p.splits * M * N, &a.P);
     if (rc) return rc;
-    a.P = static_cast<float*>(ctx->ws);
     a.split = 1;
   }
   if (a_kcontig && b_kcontig)
@@ -400,10 +518,7 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
     launch_layout<false, false>(a, p, vec, ctx->stream);
   AUR_LAUNCH_CHECK(ctx, "gemm_f32_mfma");
   if (p.splits > 1) {
-    const size_t total = (size_t)M * N;
-    int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
-    hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, a.P, C, M, N, ldc,
-                       p.splits, epi);
+    reduce_partials(ctx, a.P, C, M, N, ldc, p.splits, epi);
     AUR_LAUNCH_CHECK(ctx, "splitk_reduce");
   }
   return 0;
@@ -413,7 +528,15 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
          int ldb, float* C, int ldc, int M, int N, int K, bool accumulate) {
   Epilogue e;
   e.mode = accumulate ? EPI_ACCUM : EPI_STORE;
-  return gemm(ctx, a_kcontig, b_kcontig, A, lda, B, ldb, C, ldc, M, N, K, e);
+  return gemm(ctx, a_kcontig, b_kcontig, A, lda, B, ldb, C, ldc, M, N, K, e, nullptr);
+}
+
+int gemm_nt_partials(aur_ctx* ctx, const float* A, int lda, const float* B, int ldb, float* P, int M, int N,
+                     int K, int splits) {
+  if (M < 1 || M > 64 || N < 1 || K < 16 * splits || splits < 1 || (K & 3) || (lda & 3) || (ldb & 3) ||
+      !aligned16(A) || !aligned16(B) || !P)
+    return set_error(ctx, AUR_EINVAL, "gemm_nt_partials: unsupported shape or alignment");
+  return skinny_nt(ctx, A, lda, B, ldb, nullptr, 0, M, N, K, Epilogue{}, P, splits);
 }
 
 }  // namespace aur

@@ -27,7 +27,7 @@ constexpr float LOG2E = 1.4426950408889634f;
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
 
 struct KvArgs {
-  const float* q;       // [B, ld] rows, head h at h*d_head
+  const float* q;       // [B, ld_q] rows, head h at h*d_head
   const float* kh;      // [B, max_len, ld]
   const float* vh;
   float* out;           // [B, ld]
@@ -35,12 +35,32 @@ struct KvArgs {
   const int32_t* t_dev; // per-sequence lengths (device) or null
   int t_scalar;         // length when t_dev is null
   int ld;               // row stride of the history and out (= n_head * d_head)
-  int ld_q;             // row stride of q (d, or 3d inside a fused qkv row)
+  int ld_q;             // row stride of q, knew, vnew (d, or 3d inside a fused qkv row)
   int max_len;
   int H;
   int nch;
   float scale;
+  // Fused append (decode step): the newest key/value row (position T-1) is
+  // read from knew/vnew instead of the history, and the chunk block that
+  // owns it writes it into the history.  Null: the history already has it.
+  const float* knew;
+  const float* vnew;
 };
+
+// out[b, h*DH + d] = Σ_c 2^(m_c − M) o_c[d] / Σ_c 2^(m_c − M) l_c, c ascending.
+template <int DH>
+__device__ __forceinline__ void merge_chunks(const KvArgs& a, int b, int h, int d) {
+  const float* rec = a.ws + ((size_t)b * a.H + h) * a.nch * PART;
+  float M = -INFINITY;
+  for (int c = 0; c < a.nch; ++c) M = fmaxf(M, rec[c * PART]);
+  float L = 0.f, o = 0.f;
+  for (int c = 0; c < a.nch; ++c) {
+    const float f = exp2f(rec[c * PART] - M);
+    L += f * rec[c * PART + 1];
+    o += f * rec[c * PART + 4 + d];
+  }
+  a.out[(size_t)b * a.ld + h * DH + d] = L > 0.f ? o / L : 0.f;
+}
 
 // DH/4 lanes cover one K/V row (LPK), so one wave load instruction covers
 // KPS = 64/LPK keys.
@@ -58,92 +78,94 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
   float* rec = a.ws + (((size_t)b * a.H + h) * a.nch + c) * PART;
   if (c0 >= T) {  // chunk past this sequence's end: neutral record
     if (tid < PART) rec[tid] = tid == 0 ? -INFINITY : 0.f;
-    return;
-  }
-  const size_t hist = (size_t)b * a.max_len;
-  floatx4 qv = *reinterpret_cast<const floatx4*>(a.q + (size_t)b * a.ld_q + h * DH + 4 * part);
-  qv *= a.scale * LOG2E;
+  } else {
+    const size_t hist = (size_t)b * a.max_len;
+    floatx4 qv = *reinterpret_cast<const floatx4*>(a.q + (size_t)b * a.ld_q + h * DH + 4 * part);
+    qv *= a.scale * LOG2E;
 
-  // Scores of this wave's keys, KPS per step (one per LPK-lane group).
-  float s_loc[KPW / KPS];
+    // Every K and V row of this wave's keys is requested before any math, so
+    // the block has its whole 2·KC·DH·4-byte share of HBM traffic in flight.
+    floatx4 kreg[KPW / KPS], vreg[KPW / KPS];
 #pragma unroll
-  for (int it = 0; it < KPW / KPS; ++it) {
-    const int key = c0 + w * KPW + KPS * it + g;
-    float s = 0.f;
-    if (key < T) {
-      const floatx4 kv = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + h * DH + 4 * part);
-      s = qv[0] * kv[0] + qv[1] * kv[1] + qv[2] * kv[2] + qv[3] * kv[3];
+    for (int it = 0; it < KPW / KPS; ++it) {
+      const int key = c0 + w * KPW + KPS * it + g;
+      floatx4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+      if (key < T) {
+        if (a.knew && key == T - 1) {
+          const size_t o = (size_t)b * a.ld_q + h * DH + 4 * part;
+          kv = *reinterpret_cast<const floatx4*>(a.knew + o);
+          vv = *reinterpret_cast<const floatx4*>(a.vnew + o);
+          *reinterpret_cast<floatx4*>(const_cast<float*>(a.kh) + (hist + key) * a.ld + h * DH + 4 * part) = kv;
+          *reinterpret_cast<floatx4*>(const_cast<float*>(a.vh) + (hist + key) * a.ld + h * DH + 4 * part) = vv;
+        } else {
+          kv = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + h * DH + 4 * part);
+          vv = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + h * DH + 4 * part);
+        }
+      }
+      kreg[it] = kv;
+      vreg[it] = vv;
     }
-    s_loc[it] = s;
-  }
+    // Scores of this wave's keys, KPS per step (one per LPK-lane group).
+    float s_loc[KPW / KPS];
 #pragma unroll
-  for (int it = 0; it < KPW / KPS; ++it) {
-    float s = s_loc[it];
-#pragma unroll
-    for (int m = LPK / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
-    const int kl = w * KPW + KPS * it + g;
-    if (part == 0) sc[kl] = (c0 + kl < T) ? s : -INFINITY;
-  }
-  __syncthreads();
-
-  // Chunk max and exp-sum (log2 domain).
-  float v = tid < KC ? sc[tid] : -INFINITY;
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, shfl_xor(v, o));
-  if (lane == 0) red[w] = v;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  float e = 0.f;
-  if (tid < KC) {
-    e = exp2f(sc[tid] - M);
-    sc[tid] = e;
-  }
-  float sum = e;
-  for (int o = 32; o >= 1; o >>= 1) sum += shfl_xor(sum, o);
-  if (lane == 0) red[w] = sum;
-  __syncthreads();
-  const float L = (red[0] + red[1]) + (red[2] + red[3]);
-
-  // Unnormalised Σ_j p_j v_j over this wave's keys, 4 dims per lane.
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int it = 0; it < KPW / KPS; ++it) {
-    const int kl = w * KPW + KPS * it + g;
-    const int key = c0 + kl;
-    if (key < T) {
-      const floatx4 vv = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + h * DH + 4 * part);
-      acc += sc[kl] * vv;
+    for (int it = 0; it < KPW / KPS; ++it) {
+      const floatx4 kv = kreg[it];
+      s_loc[it] = qv[0] * kv[0] + qv[1] * kv[1] + qv[2] * kv[2] + qv[3] * kv[3];
     }
-  }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int it = 0; it < KPW / KPS; ++it) {
+      float s = s_loc[it];
 #pragma unroll
-    for (int m = LPK; m < 64; m <<= 1) acc[i] += shfl_xor(acc[i], m);
-  if (g == 0) *reinterpret_cast<floatx4*>(&obuf[w][4 * part]) = acc;
-  __syncthreads();
-  if (tid < DH) {
-    rec[4 + tid] = (obuf[0][tid] + obuf[1][tid]) + (obuf[2][tid] + obuf[3][tid]);
-    if (tid == 0) {
-      rec[0] = M;
-      rec[1] = L;
+      for (int m = LPK / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
+      const int kl = w * KPW + KPS * it + g;
+      if (part == 0) sc[kl] = (c0 + kl < T) ? s : -INFINITY;
+    }
+    __syncthreads();
+
+    // Chunk max and exp-sum (log2 domain).
+    float v = tid < KC ? sc[tid] : -INFINITY;
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, shfl_xor(v, o));
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float e = 0.f;
+    if (tid < KC) {
+      e = exp2f(sc[tid] - M);
+      sc[tid] = e;
+    }
+    float sum = e;
+    for (int o = 32; o >= 1; o >>= 1) sum += shfl_xor(sum, o);
+    if (lane == 0) red[w] = sum;
+    __syncthreads();
+    const float L = (red[0] + red[1]) + (red[2] + red[3]);
+
+    // Unnormalised Σ_j p_j v_j over this wave's keys, 4 dims per lane.
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int it = 0; it < KPW / KPS; ++it) {
+      const int kl = w * KPW + KPS * it + g;
+      acc += sc[kl] * vreg[it];  // sc = 0 for keys >= T (exp2(-inf))
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int m = LPK; m < 64; m <<= 1) acc[i] += shfl_xor(acc[i], m);
+    if (g == 0) *reinterpret_cast<floatx4*>(&obuf[w][4 * part]) = acc;
+    __syncthreads();
+    if (tid < DH) {
+      rec[4 + tid] = (obuf[0][tid] + obuf[1][tid]) + (obuf[2][tid] + obuf[3][tid]);
+      if (tid == 0) {
+        rec[0] = M;
+        rec[1] = L;
+      }
     }
   }
 }
 
-// out[b, h*DH + d] = Σ_c 2^(m_c − M) o_c[d] / Σ_c 2^(m_c − M) l_c, c ascending.
 template <int DH>
 __global__ void __launch_bounds__(64) kv_combine_kernel(KvArgs a) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const float* rec = a.ws + ((size_t)b * a.H + h) * a.nch * PART;
-  float M = -INFINITY;
-  for (int c = 0; c < a.nch; ++c) M = fmaxf(M, rec[c * PART]);
-  float L = 0.f, o = 0.f;
-  for (int c = 0; c < a.nch; ++c) {
-    const float f = exp2f(rec[c * PART] - M);
-    L += f * rec[c * PART + 1];
-    o += f * rec[c * PART + 4 + d];
-  }
-  a.out[(size_t)b * a.ld + h * DH + d] = L > 0.f ? o / L : 0.f;
+  merge_chunks<DH>(a, blockIdx.y, blockIdx.x, threadIdx.x);
 }
 
 // Launches ceil(t_max / KC) chunks per (head, sequence); t_max must be at
@@ -212,19 +234,20 @@ namespace aur {
 
 int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_history,
                    const float* v_history, float* out, float* scratch, const int32_t* t_total, int t_max,
-                   int b, int n_head, int d_head, int max_len) {
+                   int b, int n_head, int d_head, int max_len, const float* k_new, const float* v_new) {
   if (!dh_ok((uint32_t)d_head))
     return set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%d, supports 8/16/32/64", d_head);
   if (b <= 0 || n_head <= 0 || t_max <= 0 || t_max > max_len || ld_q < n_head * d_head || (ld_q & 3))
     return set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: b=%d t_max=%d max_len=%d ld_q=%d", b, t_max,
                      max_len, ld_q);
-  if (!q || !k_history || !v_history || !out || !scratch || !t_total)
+  if (!q || !k_history || !v_history || !out || !scratch || !t_total || (!k_new != !v_new))
     return set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: null pointer");
   KvArgs a{};
   a.q = q; a.kh = k_history; a.vh = v_history; a.out = out; a.ws = scratch;
   a.t_dev = t_total; a.t_scalar = 0;
   a.ld = n_head * d_head; a.ld_q = ld_q; a.max_len = max_len; a.H = n_head;
   a.scale = 1.0f / sqrtf((float)d_head);
+  a.knew = k_new; a.vnew = v_new;
   return launch(ctx, a, b, t_max, d_head);
 }
 

@@ -441,8 +441,10 @@ KvCacheGpu::KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch_, uint
   const size_t B = batch, d = d_model, F = c.d_ff, V = c.vocab;
   const size_t hist = (size_t)n_layer * B * max_len * d;
   const size_t scratch = (aur_mha_kv_ws_bytes(batch, c.n_head, max_len) + 3) / 4;
+  // K-range partial products of the W_o / W_proj decode GEMMs: ≤ 4 × [B, d].
+  part_floats_ = 4 * B * d;
   // x, ln, qkv (3), attn, xmid = 7 rows of d per sequence
-  const size_t floats = 2 * hist + B * (d * 7 + 2 * F + V) + scratch;
+  const size_t floats = 2 * hist + B * (d * 7 + 2 * F + V) + scratch + part_floats_;
   bytes_ = floats * 4 + 3 * B * 4 + 32 * 256;
   ck(ctx_, aur_malloc(ctx_, bytes_, &mem_), "KvCacheGpu alloc");
   Carver cv{static_cast<char*>(mem_)};
@@ -457,6 +459,7 @@ KvCacheGpu::KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch_, uint
   hpost_ = cv.take<float>(B * F);
   logits_ = cv.take<float>(B * V);
   scratch_ = cv.take<float>(scratch);
+  part_ = cv.take<float>(part_floats_);
   pos_ = cv.take<int32_t>(B);
   lens_ = cv.take<int32_t>(B);
   tok_ = cv.take<uint32_t>(B);
@@ -465,6 +468,7 @@ KvCacheGpu::KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch_, uint
 }
 
 KvCacheGpu::~KvCacheGpu() {
+  if (graph_) hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_));
   if (mem_) aur_free(ctx_, mem_);
 }
 
@@ -493,55 +497,123 @@ void DecoderTransformerGpu::prefill_kv(KvCacheGpu& cache, const uint32_t* tokens
 void DecoderTransformerGpu::generate_step_kv(KvCacheGpu& cache, const uint32_t* tokens, float* logits_host,
                                              uint32_t* next_tokens_host) {
   if (cache.current_len >= cache.max_len) throw Error("generate_step_kv: cache full", AUR_ELIMIT);
-  auto& A = *acts_;
-  const int B = (int)cache.batch, d = (int)cfg_.d_model, F = (int)cfg_.d_ff, V = (int)cfg_.vocab;
-  const int H = (int)cfg_.n_head, dh = d / H;
+  const int B = (int)cache.batch, V = (int)cfg_.vocab;
   if (tokens) {
     for (int i = 0; i < B; ++i)
       if (tokens[i] >= cfg_.vocab) throw Error("token id out of vocab", AUR_EINVAL);
     ck(ctx_, aur_h2d(ctx_, cache.tok_, tokens, (size_t)B * 4), "upload step tokens");
   }
+  hipStream_t st = static_cast<hipStream_t>(aur_stream(ctx_));
+  if (cache.batch <= 64) {
+    // One decode step is ~100 small launches: capture it once as a HIP graph
+    // (all pointers and shapes are fixed per cache; positions live on the
+    // device) and replay it, so the host issues one launch per step.
+    if (!cache.graph_) {
+      if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess)
+        throw Error("generate_step_kv: hipStreamBeginCapture failed", AUR_EINVAL);
+      try {
+        encode_decode_step(cache);
+      } catch (...) {
+        hipGraph_t g = nullptr;
+        hipStreamEndCapture(st, &g);
+        if (g) hipGraphDestroy(g);
+        throw;
+      }
+      hipGraph_t g = nullptr;
+      if (hipStreamEndCapture(st, &g) != hipSuccess || !g)
+        throw Error("generate_step_kv: hipStreamEndCapture failed", AUR_EINVAL);
+      hipGraphExec_t ex = nullptr;
+      const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+      hipGraphDestroy(g);
+      if (e != hipSuccess) throw Error("generate_step_kv: hipGraphInstantiate failed", (int)e);
+      cache.graph_ = ex;
+    }
+    const hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(cache.graph_), st);
+    if (e != hipSuccess) throw Error(std::string("hipGraphLaunch: ") + hipGetErrorString(e), (int)e);
+  } else {
+    encode_decode_step(cache);
+  }
+  cache.current_len += 1;
+  if (logits_host) ck(ctx_, aur_d2h(ctx_, logits_host, cache.logits_, (size_t)B * V * 4), "download logits");
+  if (next_tokens_host) ck(ctx_, aur_d2h(ctx_, next_tokens_host, cache.tok_, (size_t)B * 4), "download tokens");
+}
+
+// Enqueues one decode step for every sequence of `cache`: it reads the input
+// token ids and positions from the device (cache.tok_, cache.pos_), leaves the
+// logits and their argmax in cache.logits_ / cache.tok_ and advances the
+// positions — nothing depends on host values that change between steps.
+void DecoderTransformerGpu::encode_decode_step(KvCacheGpu& cache) {
+  auto& A = *acts_;
+  const int B = (int)cache.batch, d = (int)cfg_.d_model, F = (int)cfg_.d_ff, V = (int)cfg_.vocab;
+  const int H = (int)cfg_.n_head, dh = d / H;
+  aur::Epilogue store;
+  // The two N = d projections (W_o, W_proj) have the fewest output columns:
+  // with B ≤ 64 rows they are split into K ranges whose partial products the
+  // following LayerNorm sums (with the residual add) — more blocks in flight
+  // and no separate reduction launch.
+  const bool split = cache.batch <= 64;
+  const int s_o = std::max(1, std::min(4, d / 16)), s_p = std::max(1, std::min(4, F / 16));
   // h = w_tok[tok] + w_pos[pos]  (kv_cache.rs:103-115)
   ck(ctx_, aur::embed_forward(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, 0, cache.x_, B, d), "embed");
   ck(ctx_, aur::lens_from_pos(ctx_, cache.pos_, cache.lens_, B), "lens");
-  const int t_max = (int)cache.current_len + 1;
+  // Every chunk up to max_len is launched; chunks past a sequence's length
+  // exit at once, so the launch shape is the same for every step.
+  const int t_max = (int)cache.max_len;
   for (uint32_t l = 0; l < cfg_.n_layer; ++l) {
     Layer& Y = (*layers_)[l];
     // block_step (kv_cache.rs:147-245) for B sequences at once
-    ck(ctx_, aur::layer_norm_forward(ctx_, cache.x_, Y.ln1_g, Y.ln1_b, cache.ln_, nullptr, nullptr, B, d,
-                                     kLnEps),
-       "ln1");
-    ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, Y.w_qkv, d, cache.qkv_, 3 * d, B, 3 * d, d, false), "qkv");
-    ck(ctx_, aur::kv_store(ctx_, cache.qkv_, d, cache.k_history(l), cache.v_history(l), (int)cache.max_len,
-                           cache.pos_, B, 0),
-       "kv append");
+    if (split && l > 0)  // x = xmid + proj partials of the previous layer
+      ck(ctx_, aur::layer_norm_forward_sum(ctx_, cache.xmid_, cache.part_, s_p, cache.x_, Y.ln1_g, Y.ln1_b,
+                                           cache.ln_, B, d, kLnEps),
+         "ln1");
+    else
+      ck(ctx_, aur::layer_norm_forward(ctx_, cache.x_, Y.ln1_g, Y.ln1_b, cache.ln_, nullptr, nullptr, B, d,
+                                       kLnEps),
+         "ln1");
+    ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, Y.w_qkv, d, cache.qkv_, 3 * d, B, 3 * d, d, store), "qkv");
+    // attention of the new query over history + the new row, which the
+    // kernel also appends to the history (kv_cache.rs:169-179)
     ck(ctx_, aur::mha_kv_batched(ctx_, cache.qkv_, 3 * d, cache.k_history(l), cache.v_history(l), cache.attn_,
-                                 cache.scratch_, cache.lens_, t_max, B, H, dh, (int)cache.max_len),
+                                 cache.scratch_, cache.lens_, t_max, B, H, dh, (int)cache.max_len,
+                                 cache.qkv_ + d, cache.qkv_ + 2 * d),
        "mha_kv");
-    aur::Epilogue resid;
-    resid.mode = aur::EPI_RESID;
-    resid.R = cache.x_;
-    ck(ctx_, aur::gemm(ctx_, true, true, cache.attn_, d, Y.w_o, d, cache.xmid_, d, B, d, d, resid), "w_o");
-    ck(ctx_, aur::layer_norm_forward(ctx_, cache.xmid_, Y.ln2_g, Y.ln2_b, cache.ln_, nullptr, nullptr, B, d,
-                                     kLnEps),
-       "ln2");
+    if (split) {
+      ck(ctx_, aur::gemm_nt_partials(ctx_, cache.attn_, d, Y.w_o, d, cache.part_, B, d, d, s_o), "w_o");
+      ck(ctx_, aur::layer_norm_forward_sum(ctx_, cache.x_, cache.part_, s_o, cache.xmid_, Y.ln2_g, Y.ln2_b,
+                                           cache.ln_, B, d, kLnEps),
+         "ln2");
+    } else {
+      aur::Epilogue resid;
+      resid.mode = aur::EPI_RESID;
+      resid.R = cache.x_;
+      ck(ctx_, aur::gemm(ctx_, true, true, cache.attn_, d, Y.w_o, d, cache.xmid_, d, B, d, d, resid), "w_o");
+      ck(ctx_, aur::layer_norm_forward(ctx_, cache.xmid_, Y.ln2_g, Y.ln2_b, cache.ln_, nullptr, nullptr, B, d,
+                                       kLnEps),
+         "ln2");
+    }
     aur::Epilogue ge;
     ge.mode = aur::EPI_GELU;
     ge.C2 = cache.hpost_;
     ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, Y.w_fc, d, cache.hpre_, F, B, F, d, ge), "w_fc");
-    aur::Epilogue r2;
-    r2.mode = aur::EPI_RESID;
-    r2.R = cache.xmid_;
-    ck(ctx_, aur::gemm(ctx_, true, true, cache.hpost_, F, Y.w_proj, F, cache.x_, d, B, d, F, r2), "w_proj");
+    if (split) {
+      ck(ctx_, aur::gemm_nt_partials(ctx_, cache.hpost_, F, Y.w_proj, F, cache.part_, B, d, F, s_p), "w_proj");
+    } else {
+      aur::Epilogue r2;
+      r2.mode = aur::EPI_RESID;
+      r2.R = cache.xmid_;
+      ck(ctx_, aur::gemm(ctx_, true, true, cache.hpost_, F, Y.w_proj, F, cache.x_, d, B, d, F, r2), "w_proj");
+    }
   }
-  ck(ctx_, aur::layer_norm_forward(ctx_, cache.x_, A.lnf_g, A.lnf_b, cache.ln_, nullptr, nullptr, B, d, kLnEps),
-     "lnf");
-  ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, A.w_tok, d, cache.logits_, V, B, V, d, false), "head");
-  ck(ctx_, aur::argmax_rows(ctx_, cache.logits_, B, V, cache.tok_), "argmax");
-  ck(ctx_, aur::advance_pos(ctx_, cache.pos_, B), "advance pos");
-  cache.current_len += 1;
-  if (logits_host) ck(ctx_, aur_d2h(ctx_, logits_host, cache.logits_, (size_t)B * V * 4), "download logits");
-  if (next_tokens_host) ck(ctx_, aur_d2h(ctx_, next_tokens_host, cache.tok_, (size_t)B * 4), "download tokens");
+  if (split)
+    ck(ctx_, aur::layer_norm_forward_sum(ctx_, cache.xmid_, cache.part_, s_p, cache.x_, A.lnf_g, A.lnf_b,
+                                         cache.ln_, B, d, kLnEps),
+       "lnf");
+  else
+    ck(ctx_, aur::layer_norm_forward(ctx_, cache.x_, A.lnf_g, A.lnf_b, cache.ln_, nullptr, nullptr, B, d,
+                                     kLnEps),
+       "lnf");
+  ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, A.w_tok, d, cache.logits_, V, B, V, d, store), "head");
+  ck(ctx_, aur::argmax_rows(ctx_, cache.logits_, B, V, cache.tok_, cache.pos_), "argmax");
 }
 
 }  // namespace aurora

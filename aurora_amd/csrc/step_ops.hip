@@ -121,6 +121,100 @@ __global__ void __launch_bounds__(256) ln_fwd_kernel(const float* __restrict__ x
   }
 }
 
+// The same for few rows (decode: one row per sequence): one 256-thread block
+// per row, float4 traffic, so a launch over 32 rows is not latency-bound.
+// Requires d % 4 == 0 and 16-byte aligned rows.
+__global__ void __launch_bounds__(256) ln_fwd_rowblock_kernel(const float* __restrict__ x,
+                                                              const float* __restrict__ gamma,
+                                                              const float* __restrict__ beta,
+                                                              float* __restrict__ y,
+                                                              float* __restrict__ mean,
+                                                              float* __restrict__ rstd, int d,
+                                                              float eps) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const float* xr = x + (size_t)r * d;
+  float s = 0.f;
+  for (int c = threadIdx.x * 4; c < d; c += 1024) {
+    const floatx4 v = *reinterpret_cast<const floatx4*>(xr + c);
+    s += (v[0] + v[1]) + (v[2] + v[3]);
+  }
+  const float mu = block_sum(s, red) / (float)d;
+  float q = 0.f;
+  for (int c = threadIdx.x * 4; c < d; c += 1024) {
+    const floatx4 v = *reinterpret_cast<const floatx4*>(xr + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q += (v[e] - mu) * (v[e] - mu);
+  }
+  const float is = 1.0f / sqrtf(block_sum(q, red) / (float)d + eps);
+  float* yr = y + (size_t)r * d;
+  for (int c = threadIdx.x * 4; c < d; c += 1024) {
+    const floatx4 v = *reinterpret_cast<const floatx4*>(xr + c);
+    const floatx4 gg = *reinterpret_cast<const floatx4*>(gamma + c);
+    const floatx4 bb = *reinterpret_cast<const floatx4*>(beta + c);
+    floatx4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (v[e] - mu) * is * gg[e] + bb[e];
+    *reinterpret_cast<floatx4*>(yr + c) = o;
+  }
+  if (threadIdx.x == 0) {
+    if (mean) mean[r] = mu;
+    if (rstd) rstd[r] = is;
+  }
+}
+
+// Decode-step LayerNorm that first completes the residual add of a split-K
+// projection: x = R + (P[0] + P[1] + … + P[np−1]) (ranges in order, the
+// product summed before the residual is added, as an unsplit GEMM's
+// epilogue would), writes x (the residual stream) and y = LN(x).  One block
+// per row; each thread keeps its ≤ 4 float4 of the row in registers.
+__global__ void __launch_bounds__(256) ln_fwd_sum_kernel(const float* __restrict__ R,
+                                                         const float* __restrict__ P, int np,
+                                                         size_t pstride, float* __restrict__ xo,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ beta,
+                                                         float* __restrict__ y, int d, float eps) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  floatx4 xv[4];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (threadIdx.x + 256 * i) * 4;
+    floatx4 v = {0.f, 0.f, 0.f, 0.f};
+    if (c < d) {
+      floatx4 acc = *reinterpret_cast<const floatx4*>(P + (size_t)r * d + c);
+      for (int z = 1; z < np; ++z) acc += *reinterpret_cast<const floatx4*>(P + z * pstride + (size_t)r * d + c);
+      v = *reinterpret_cast<const floatx4*>(R + (size_t)r * d + c) + acc;
+      *reinterpret_cast<floatx4*>(xo + (size_t)r * d + c) = v;
+      s += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+    xv[i] = v;
+  }
+  const float mu = block_sum(s, red) / (float)d;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (threadIdx.x + 256 * i) * 4;
+    if (c < d)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q += (xv[i][e] - mu) * (xv[i][e] - mu);
+  }
+  const float is = 1.0f / sqrtf(block_sum(q, red) / (float)d + eps);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (threadIdx.x + 256 * i) * 4;
+    if (c < d) {
+      const floatx4 gg = *reinterpret_cast<const floatx4*>(gamma + c);
+      const floatx4 bb = *reinterpret_cast<const floatx4*>(beta + c);
+      floatx4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (xv[i][e] - mu) * is * gg[e] + bb[e];
+      *reinterpret_cast<floatx4*>(y + (size_t)r * d + c) = o;
+    }
+  }
+}
+
 // dx = s·(g − (Σg + x̂·Σ(g·x̂))/d) [+ dres],  g = dy·γ,  x̂ = (x − mu)·s.
 __global__ void __launch_bounds__(256) ln_bwd_kernel(const float* __restrict__ x,
                                                      const float* __restrict__ mean,
@@ -318,14 +412,11 @@ __global__ void lens_from_pos_kernel(const int32_t* __restrict__ pos, int32_t* _
   if (b < B) lens[b] = pos[b] + 1;
 }
 
-__global__ void advance_pos_kernel(int32_t* __restrict__ pos, int B) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b < B) pos[b] += 1;
-}
-
 // First index of the row maximum (src/transformer/loss.rs argmax: strict >).
+// pos (optional): the row's sequence position is advanced by one — the end
+// of a decode step.
 __global__ void __launch_bounds__(256) argmax_kernel(const float* __restrict__ logits, int V,
-                                                     uint32_t* __restrict__ out) {
+                                                     uint32_t* __restrict__ out, int32_t* __restrict__ pos) {
   __shared__ float sv[256];
   __shared__ int si[256];
   const int r = blockIdx.x;
@@ -353,7 +444,10 @@ __global__ void __launch_bounds__(256) argmax_kernel(const float* __restrict__ l
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) out[r] = (uint32_t)(si[0] == 0x7fffffff ? 0 : si[0]);
+  if (threadIdx.x == 0) {
+    out[r] = (uint32_t)(si[0] == 0x7fffffff ? 0 : si[0]);
+    if (pos) pos[r] += 1;
+  }
 }
 
 __global__ void gather_rows_kernel(const float* __restrict__ src, int ld_src, int row_step,
@@ -392,9 +486,25 @@ int embed_backward(aur_ctx* ctx, const float* dy, int B, int T, int d, const uin
 
 int layer_norm_forward(aur_ctx* ctx, const float* x, const float* gamma, const float* beta, float* y,
                        float* mean, float* rstd, int rows, int d, float eps) {
-  hipLaunchKernelGGL(ln_fwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, ctx->stream, x, gamma, beta, y,
-                     mean, rstd, rows, d, eps);
+  const bool vec = d % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+                                   reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) &
+                                  15) == 0;
+  if (rows < 1024 && vec)
+    hipLaunchKernelGGL(ln_fwd_rowblock_kernel, dim3(rows), dim3(256), 0, ctx->stream, x, gamma, beta, y, mean,
+                       rstd, d, eps);
+  else
+    hipLaunchKernelGGL(ln_fwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, ctx->stream, x, gamma, beta, y,
+                       mean, rstd, rows, d, eps);
   LAUNCH_OK(ctx, "ln_fwd_kernel");
+}
+
+int layer_norm_forward_sum(aur_ctx* ctx, const float* R, const float* P, int np, float* x_out,
+                           const float* gamma, const float* beta, float* y, int rows, int d, float eps) {
+  if (d % 4 != 0 || d > 4096 || np < 1)
+    return set_error(ctx, AUR_EINVAL, "layer_norm_forward_sum: d=%d np=%d unsupported", d, np);
+  hipLaunchKernelGGL(ln_fwd_sum_kernel, dim3(rows), dim3(256), 0, ctx->stream, R, P, np, (size_t)rows * d,
+                     x_out, gamma, beta, y, d, eps);
+  LAUNCH_OK(ctx, "ln_fwd_sum_kernel");
 }
 
 size_t layer_norm_backward_ws_floats(int rows, int d) {
@@ -458,13 +568,8 @@ int lens_from_pos(aur_ctx* ctx, const int32_t* pos, int32_t* lens, int B) {
   LAUNCH_OK(ctx, "lens_from_pos_kernel");
 }
 
-int advance_pos(aur_ctx* ctx, int32_t* pos, int B) {
-  hipLaunchKernelGGL(advance_pos_kernel, dim3((B + 255) / 256), dim3(256), 0, ctx->stream, pos, B);
-  LAUNCH_OK(ctx, "advance_pos_kernel");
-}
-
-int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, ctx->stream, logits, V, out);
+int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out, int32_t* pos) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, ctx->stream, logits, V, out, pos);
   LAUNCH_OK(ctx, "argmax_kernel");
 }
 

@@ -16,6 +16,10 @@ int embed_backward(aur_ctx* ctx, const float* dy, int B, int T, int d, const uin
 
 int layer_norm_forward(aur_ctx* ctx, const float* x, const float* gamma, const float* beta, float* y,
                        float* mean, float* rstd, int rows, int d, float eps);
+// x = R + Σ_{z<np} P[z] (P: [np][rows][d], summed in z order), x_out = x,
+// y = LN(x).  d % 4 == 0, d <= 4096.
+int layer_norm_forward_sum(aur_ctx* ctx, const float* R, const float* P, int np, float* x_out,
+                           const float* gamma, const float* beta, float* y, int rows, int d, float eps);
 size_t layer_norm_backward_ws_floats(int rows, int d);
 // dx = LN'(dy) [+ dres]; dgamma/dbeta accumulated (fixed-order column sums in ws).
 int layer_norm_backward(aur_ctx* ctx, const float* x, const float* mean, const float* rstd,
@@ -37,15 +41,18 @@ int adamw(aur_ctx* ctx, float* p, const float* g, float* m1, float* m2, size_t n
 int kv_store(aur_ctx* ctx, const float* qkv, int d, float* kh, float* vh, int max_len,
              const int32_t* pos_dev, int rows, int T);
 int lens_from_pos(aur_ctx* ctx, const int32_t* pos, int32_t* lens, int B);
-int advance_pos(aur_ctx* ctx, int32_t* pos, int B);
-int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out);
+// out[r] = first argmax of logits row r; pos[r] += 1 when pos is non-null.
+int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out, int32_t* pos = nullptr);
 // dst[r] = src[(r*row_step + row_off) * ld_src .. + d]
 int gather_rows(aur_ctx* ctx, const float* src, int ld_src, int row_step, int row_off, float* dst,
                 int rows, int d);
 
 // Batched KV decode attention with q rows of stride ld_q (kv_decode.hip).
+// k_new/v_new (same stride as q): the row at position t_total-1 is taken from
+// them and appended to the history by the kernel.
 int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_history,
                    const float* v_history, float* out, float* scratch, const int32_t* t_total, int t_max,
-                   int b, int n_head, int d_head, int max_len);
+                   int b, int n_head, int d_head, int max_len, const float* k_new = nullptr,
+                   const float* v_new = nullptr);
 
 }  // namespace aur

@@ -124,6 +124,21 @@ def test_ragged_shapes_all_forms(ctx, m, k, n):
     assert cw < TOL_GEMM and fr < TOL_GEMM, ("outer", cw, fr)
 
 
+@pytest.mark.parametrize("m,k,n", [(32, 1024, 3072), (32, 1024, 1024), (32, 4096, 1024),
+                                   (32, 1024, 8192), (1, 36, 130), (17, 4100, 100), (64, 256, 64),
+                                   (48, 2048, 200)])
+def test_decode_shaped_nt(ctx, m, k, n):
+    """M ≤ 64 A@Bᵀ (the decode projections and head) takes the skinny path:
+    with and without a K split, ragged N and M, one-chunk K."""
+    rng = np.random.default_rng(6000 + m + k + n)
+    a, b = _u(rng, m * k), _u(rng, n * k)
+    got = _nt(ctx, a, b, m, n, k)
+    cw, fr = _gates(got, a.reshape(m, k).astype(np.float64), b.reshape(n, k).T.astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
+    again = _nt(ctx, a, b, m, n, k)
+    assert np.array_equal(got, again)
+
+
 def test_k_zero_overwrites_and_accumulate_keeps(ctx):
     from aurora_amd.gpu import GpuBuffer
 
