@@ -115,11 +115,81 @@ __device__ __forceinline__ void load_rows_frag(floatx4* f, const float* __restri
 }
 
 // ---------------------------------------------------------------- forward
+// One 64-key tile of the online softmax for this lane's query row.  qf holds
+// Q pre-multiplied by scale·log2(e), so scores are already in the log2
+// domain.  Only the diagonal tile (DIAG) needs the causal mask: every key of
+// an earlier tile precedes every query of this block.  On the diagonal tile
+// key sub-tiles j > w lie entirely in the future and are skipped.
+template <int DH, bool DIAG>
+__device__ __forceinline__ void fwd_tile(const float* __restrict__ Ks, const float* __restrict__ Vs,
+                                         const floatx4* qf, floatx4* acc_o, float& m, float& l,
+                                         int w, int g, int l16) {
+  using G = Geo<DH>;
+  constexpr int NC = G::NC, LDT = G::LDT;
+  const int jmax = DIAG ? w : 3;
+  floatx4 st[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    st[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (j <= jmax) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const floatx4 kf = *reinterpret_cast<const floatx4*>(Ks + (16 * j + l16) * LDT + 16 * c + 4 * g);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) st[j] = mfma16x16x4(kf[s], qf[c][s], st[j]);
+      }
+    }
+  }
+  // st[j][e] = S[qrow][k0 + 16j + 4g + e]; on the diagonal tile the key is
+  // in the future when 16j + 4g + e > 16w + l16.
+  if (DIAG) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (j > jmax || 16 * j + 4 * g + e > 16 * w + l16) st[j][e] = -INFINITY;
+  }
+  float mx = fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3]));
+#pragma unroll
+  for (int j = 1; j < 4; ++j) mx = fmaxf(mx, fmaxf(fmaxf(st[j][0], st[j][1]), fmaxf(st[j][2], st[j][3])));
+  mx = fmaxf(mx, shfl_xor(mx, 16));
+  mx = fmaxf(mx, shfl_xor(mx, 32));
+  const float m_new = fmaxf(m, mx);
+  const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+  m = m_new;
+  float ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = __builtin_amdgcn_exp2f(st[j][e] - m_new);
+      st[j][e] = p;
+      ps += p;
+    }
+  l = l * alpha + ps;
+#pragma unroll
+  for (int d = 0; d < NC; ++d) acc_o[d] *= alpha;
+  // Oᵀ[d][q] += Vᵀ[d][key] · Pᵀ[key][q]
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j <= jmax) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float* vr = Vs + (16 * j + 4 * g + s) * LDT + l16;
+#pragma unroll
+        for (int d = 0; d < NC; ++d) acc_o[d] = mfma16x16x4(vr[16 * d], st[j][s], acc_o[d]);
+      }
+    }
+  }
+}
+
+// One block = 64 query rows of one (batch, head); one LDS stage for the K
+// and V tiles, the next tile prefetched into registers during the MFMAs.
 template <int DH>
 __global__ void __launch_bounds__(256) mha_fwd_kernel(AttnArgs a) {
   using G = Geo<DH>;
-  constexpr int NC = G::NC, LDT = G::LDT;
-  __shared__ __attribute__((aligned(16))) float sm[2][2][G::TILE];  // [stage][K,V]
+  constexpr int NC = G::NC;
+  __shared__ __attribute__((aligned(16))) float sm[2][G::TILE];  // [K,V]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, l16 = lane & 15;
   const int nqt = (a.T + TQ - 1) / TQ;
@@ -134,96 +204,34 @@ __global__ void __launch_bounds__(256) mha_fwd_kernel(AttnArgs a) {
   const int qrow = q0 + 16 * w + l16;  // this lane's query row (Sᵀ column)
   floatx4 qf[NC];
   load_rows_frag<DH>(qf, Qb, a.ld_qkv, qrow, a.T, g);
+  const float sl2 = a.scale * LOG2E;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) qf[c] *= sl2;
 
-  const float sl2 = a.scale * LOG2E;  // scores kept in the log2 domain
   float m = -INFINITY, l = 0.f;
   floatx4 acc_o[NC];
 #pragma unroll
   for (int d = 0; d < NC; ++d) acc_o[d] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  zero_pad_cols<DH>(sm[0][0], tid);
-  zero_pad_cols<DH>(sm[0][1], tid);
-  zero_pad_cols<DH>(sm[1][0], tid);
-  zero_pad_cols<DH>(sm[1][1], tid);
+  zero_pad_cols<DH>(sm[0], tid);
+  zero_pad_cols<DH>(sm[1], tid);
   TileRegs<DH> rk, rv;
   rk.load(Kb, a.ld_qkv, 0, a.T, tid);
   rv.load(Vb, a.ld_qkv, 0, a.T, tid);
-  rk.store(sm[0][0], tid);
-  rv.store(sm[0][1], tid);
+  rk.store(sm[0], tid);
+  rv.store(sm[1], tid);
   __syncthreads();
 
-  for (int kt = 0; kt <= qt; ++kt) {
-    const int cur = kt & 1;
-    if (kt < qt) {
-      rk.load(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
-      rv.load(Vb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
-    }
-    const float* Ks = sm[cur][0];
-    const float* Vs = sm[cur][1];
-    const int k0 = kt * TQ;
-    // Key sub-tiles j > w of the diagonal tile are entirely in the future.
-    const int jmax = (kt == qt) ? w : 3;
-
-    floatx4 st[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      st[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (j <= jmax) {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const floatx4 kf = *reinterpret_cast<const floatx4*>(Ks + (16 * j + l16) * LDT + 16 * c + 4 * g);
-#pragma unroll
-          for (int s = 0; s < 4; ++s) st[j] = mfma16x16x4(kf[s], qf[c][s], st[j]);
-        }
-      }
-    }
-    // Scale, mask, tile row max.  st[j][e] = S[qrow][k0 + 16j + 4g + e].
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = k0 + 16 * j + 4 * g + e;
-        float s = st[j][e] * sl2;
-        if (j > jmax || key > qrow || key >= a.T) s = -INFINITY;
-        st[j][e] = s;
-        mx = fmaxf(mx, s);
-      }
-    mx = fmaxf(mx, shfl_xor(mx, 16));
-    mx = fmaxf(mx, shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = exp2f(m - m_new);
-    m = m_new;
-    float ps = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p = exp2f(st[j][e] - m_new);
-        st[j][e] = p;
-        ps += p;
-      }
-    l = l * alpha + ps;
-#pragma unroll
-    for (int d = 0; d < NC; ++d) acc_o[d] *= alpha;
-    // Oᵀ[d][q] += Vᵀ[d][key] · Pᵀ[key][q]
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j <= jmax) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const float* vr = Vs + (16 * j + 4 * g + s) * LDT + l16;
-#pragma unroll
-          for (int d = 0; d < NC; ++d) acc_o[d] = mfma16x16x4(vr[16 * d], st[j][s], acc_o[d]);
-        }
-      }
-    }
-    if (kt < qt) {
-      rk.store(sm[cur ^ 1][0], tid);
-      rv.store(sm[cur ^ 1][1], tid);
-    }
+  for (int kt = 0; kt < qt; ++kt) {
+    rk.load(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
+    rv.load(Vb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
+    fwd_tile<DH, false>(sm[0], sm[1], qf, acc_o, m, l, w, g, l16);
+    __syncthreads();  // every wave is done with the stage
+    rk.store(sm[0], tid);
+    rv.store(sm[1], tid);
     __syncthreads();
   }
+  fwd_tile<DH, true>(sm[0], sm[1], qf, acc_o, m, l, w, g, l16);
 
   l += shfl_xor(l, 16);
   l += shfl_xor(l, 32);
@@ -266,11 +274,51 @@ __global__ void __launch_bounds__(256) mha_bwd_rowdot_kernel(AttnArgs a, int B) 
 }
 
 // ---------------------------------------------------- backward pass 2: dQ
+// One 64-key tile of dQᵀ for this lane's query row.  Only the diagonal tile
+// (DIAG) is masked; keys past T only occur there and their K/V rows are zero.
+template <int DH, bool DIAG>
+__device__ __forceinline__ void dq_tile(const float* __restrict__ Ks, const float* __restrict__ Vs,
+                                        const floatx4* qf, const floatx4* df, floatx4* acc, float lse2,
+                                        float Dq, int w, int g, int l16) {
+  using G = Geo<DH>;
+  constexpr int NC = G::NC, LDT = G::LDT;
+  const int jmax = DIAG ? w : 3;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j > jmax) continue;
+    floatx4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const floatx4 kf = *reinterpret_cast<const floatx4*>(Ks + (16 * j + l16) * LDT + 16 * c + 4 * g);
+      const floatx4 vf = *reinterpret_cast<const floatx4*>(Vs + (16 * j + l16) * LDT + 16 * c + 4 * g);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        st = mfma16x16x4(kf[s], qf[c][s], st);  // Sᵀ[key][q] (log2 domain)
+        dp = mfma16x16x4(vf[s], df[c][s], dp);  // dPᵀ[key][q]
+      }
+    }
+    // dSᵀ = Pᵀ ⊙ (dPᵀ − D_q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float p = __builtin_amdgcn_exp2f(st[e] - lse2);
+      if (DIAG && 16 * j + 4 * g + e > 16 * w + l16) p = 0.f;
+      st[e] = p * (dp[e] - Dq);
+    }
+    // dQᵀ[d][q] += Kᵀ[d][key] · dSᵀ[key][q]
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float* kr = Ks + (16 * j + 4 * g + s) * LDT + l16;
+#pragma unroll
+      for (int d = 0; d < NC; ++d) acc[d] = mfma16x16x4(kr[16 * d], st[s], acc[d]);
+    }
+  }
+}
+
 template <int DH>
 __global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
   using G = Geo<DH>;
-  constexpr int NC = G::NC, LDT = G::LDT;
-  __shared__ __attribute__((aligned(16))) float sm[2][2][G::TILE];  // [stage][K,V]
+  constexpr int NC = G::NC;
+  __shared__ __attribute__((aligned(16))) float sm[2][G::TILE];  // [K,V]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, l16 = lane & 15;
   const int nqt = (a.T + TQ - 1) / TQ;
@@ -287,72 +335,37 @@ __global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
   floatx4 qf[NC], df[NC];
   load_rows_frag<DH>(qf, Qb, a.ld_qkv, qrow, a.T, g);
   load_rows_frag<DH>(df, dOb, a.ld_o, qrow, a.T, g);
+  const float sl2 = a.scale * LOG2E;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) qf[c] *= sl2;
   const size_t stat = ((size_t)b * a.H + h) * a.T;
   const float lse2 = qrow < a.T ? a.lse[stat + qrow] * LOG2E : 0.f;
   const float Dq = qrow < a.T ? a.D[stat + qrow] : 0.f;
-  const float sl2 = a.scale * LOG2E;
 
   floatx4 acc[NC];
 #pragma unroll
   for (int d = 0; d < NC; ++d) acc[d] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  zero_pad_cols<DH>(sm[0][0], tid);
-  zero_pad_cols<DH>(sm[0][1], tid);
-  zero_pad_cols<DH>(sm[1][0], tid);
-  zero_pad_cols<DH>(sm[1][1], tid);
+  zero_pad_cols<DH>(sm[0], tid);
+  zero_pad_cols<DH>(sm[1], tid);
   TileRegs<DH> rk, rv;
   rk.load(Kb, a.ld_qkv, 0, a.T, tid);
   rv.load(Vb, a.ld_qkv, 0, a.T, tid);
-  rk.store(sm[0][0], tid);
-  rv.store(sm[0][1], tid);
+  rk.store(sm[0], tid);
+  rv.store(sm[1], tid);
   __syncthreads();
 
-  for (int kt = 0; kt <= qt; ++kt) {
-    const int cur = kt & 1;
-    if (kt < qt) {
-      rk.load(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
-      rv.load(Vb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
-    }
-    const float* Ks = sm[cur][0];
-    const float* Vs = sm[cur][1];
-    const int k0 = kt * TQ;
-    const int jmax = (kt == qt) ? w : 3;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j > jmax) continue;
-      floatx4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const floatx4 kf = *reinterpret_cast<const floatx4*>(Ks + (16 * j + l16) * LDT + 16 * c + 4 * g);
-        const floatx4 vf = *reinterpret_cast<const floatx4*>(Vs + (16 * j + l16) * LDT + 16 * c + 4 * g);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          st = mfma16x16x4(kf[s], qf[c][s], st);  // Sᵀ[key][q]
-          dp = mfma16x16x4(vf[s], df[c][s], dp);  // dPᵀ[key][q]
-        }
-      }
-      // dSᵀ = Pᵀ ⊙ (dPᵀ − D_q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = k0 + 16 * j + 4 * g + e;
-        float p = exp2f(st[e] * sl2 - lse2);
-        if (key > qrow || key >= a.T) p = 0.f;
-        st[e] = p * (dp[e] - Dq);
-      }
-      // dQᵀ[d][q] += Kᵀ[d][key] · dSᵀ[key][q]
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float* kr = Ks + (16 * j + 4 * g + s) * LDT + l16;
-#pragma unroll
-        for (int d = 0; d < NC; ++d) acc[d] = mfma16x16x4(kr[16 * d], st[s], acc[d]);
-      }
-    }
-    if (kt < qt) {
-      rk.store(sm[cur ^ 1][0], tid);
-      rv.store(sm[cur ^ 1][1], tid);
-    }
+  for (int kt = 0; kt < qt; ++kt) {
+    rk.load(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
+    rv.load(Vb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
+    dq_tile<DH, false>(sm[0], sm[1], qf, df, acc, lse2, Dq, w, g, l16);
+    __syncthreads();  // every wave is done with the stage
+    rk.store(sm[0], tid);
+    rv.store(sm[1], tid);
     __syncthreads();
   }
+  dq_tile<DH, true>(sm[0], sm[1], qf, df, acc, lse2, Dq, w, g, l16);
+
   if (qrow < a.T) {
     float* dqr = a.dq + (row_base + qrow) * a.ld_d + h * DH;
 #pragma unroll
@@ -365,13 +378,13 @@ __global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
 }
 
 // ------------------------------------------------- backward pass 3: dK, dV
-template <int DH>
+template <int DH, int NS>
 __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
   using G = Geo<DH>;
   constexpr int NC = G::NC, LDT = G::LDT;
-  __shared__ __attribute__((aligned(16))) float sm[2][2][G::TILE];  // [stage][Q,dO]
-  __shared__ __attribute__((aligned(16))) float st_lse[2][TQ];
-  __shared__ __attribute__((aligned(16))) float st_D[2][TQ];
+  __shared__ __attribute__((aligned(16))) float sm[NS][2][G::TILE];  // [stage][Q,dO]
+  __shared__ __attribute__((aligned(16))) float st_lse[NS][TQ];
+  __shared__ __attribute__((aligned(16))) float st_D[NS][TQ];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, l16 = lane & 15;
   const int nqt = (a.T + TQ - 1) / TQ;
@@ -389,7 +402,11 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
   floatx4 kf[NC], vf[NC];
   load_rows_frag<DH>(kf, Kb, a.ld_qkv, krow, a.T, g);
   load_rows_frag<DH>(vf, Vb, a.ld_qkv, krow, a.T, g);
+  // K pre-multiplied by scale·log2(e): S comes out in the log2 domain.  dK
+  // is accumulated from the unscaled dS and scaled once at the end.
   const float sl2 = a.scale * LOG2E;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) kf[c] *= sl2;
 
   floatx4 acc_k[NC], acc_v[NC];
 #pragma unroll
@@ -398,10 +415,10 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
     acc_v[d] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  zero_pad_cols<DH>(sm[0][0], tid);
-  zero_pad_cols<DH>(sm[0][1], tid);
-  zero_pad_cols<DH>(sm[1][0], tid);
-  zero_pad_cols<DH>(sm[1][1], tid);
+  for (int st = 0; st < NS; ++st) {
+    zero_pad_cols<DH>(sm[st][0], tid);
+    zero_pad_cols<DH>(sm[st][1], tid);
+  }
   TileRegs<DH> rq, rd;
   float r_lse = 0.f, r_D = 0.f;
   auto load_stats = [&](int q0) {
@@ -423,7 +440,7 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
   __syncthreads();
 
   for (int qt = kt; qt < nqt; ++qt) {
-    const int cur = (qt - kt) & 1;
+    const int cur = NS == 2 ? ((qt - kt) & 1) : 0;
     const bool more = qt + 1 < nqt;
     if (more) {
       rq.load(Qb, a.ld_qkv, (qt + 1) * TQ, a.T, tid);
@@ -456,8 +473,8 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int q = q0 + 16 * jq + 4 * g + e;
-        float pe = exp2f(s_[e] * sl2 - lq[e]);
-        if (krow > q || q >= a.T) pe = 0.f;
+        float pe = __builtin_amdgcn_exp2f(s_[e] - lq[e]);
+        if (qt == kt && krow > q) pe = 0.f;
         p[e] = pe;
         ds[e] = pe * (dp[e] - Dq[e]);
       }
@@ -474,11 +491,12 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
       }
     }
     if (more) {
-      rq.store(sm[cur ^ 1][0], tid);
-      rd.store(sm[cur ^ 1][1], tid);
+      if (NS == 1) __syncthreads();  // every wave is done with the only stage
+      rq.store(sm[(cur + 1) % NS][0], tid);
+      rd.store(sm[(cur + 1) % NS][1], tid);
       if (tid < TQ) {
-        st_lse[cur ^ 1][tid] = r_lse;
-        st_D[cur ^ 1][tid] = r_D;
+        st_lse[(cur + 1) % NS][tid] = r_lse;
+        st_D[(cur + 1) % NS][tid] = r_D;
       }
     }
     __syncthreads();
@@ -515,7 +533,7 @@ int check_common(aur_ctx* ctx, uint32_t b, uint32_t t, uint32_t n_head, uint32_t
 template <int DH>
 void launch_fwd(const AttnArgs& a, int b, hipStream_t st) {
   dim3 grid((a.T + TQ - 1) / TQ, a.H, b);
-  hipLaunchKernelGGL(mha_fwd_kernel<DH>, grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((mha_fwd_kernel<DH>), grid, dim3(256), 0, st, a);
 }
 
 template <int DH>
@@ -525,8 +543,8 @@ void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
   hipLaunchKernelGGL(mha_bwd_rowdot_kernel<DH>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256),
                      0, st, a, b);
   dim3 grid((a.T + TQ - 1) / TQ, a.H, b);
-  hipLaunchKernelGGL(mha_bwd_dq_kernel<DH>, grid, dim3(256), 0, st, a);
-  hipLaunchKernelGGL(mha_bwd_dkv_kernel<DH>, grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((mha_bwd_dq_kernel<DH>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((mha_bwd_dkv_kernel<DH, 2>), grid, dim3(256), 0, st, a);
 }
 
 }  // namespace
