@@ -175,12 +175,19 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
   const int g16 = lane >> 4, l16 = lane & 15;
 
   // XCD-aware tile order: consecutive workgroups are dispatched round-robin
-  // over the 8 XCDs; give each XCD a contiguous run of tiles so that tiles
-  // sharing an A row panel hit the same L2.
+  // over the 8 XCDs; give each XCD a contiguous run of tiles, and walk that
+  // run in groups of GM tile rows, column by column, so the ~64 tiles an
+  // XCD runs at once form a GM × 8 block: each A and B panel slice is
+  // fetched into that XCD's L2 once for 8 tiles instead of once per tile
+  // (row-major order would stream every B panel through L2 per tile row).
+  constexpr int GM = 8;
   const int ntiles = g.tiles_m * g.tiles_n;
   int pid = blockIdx.x;
   if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
-  const int tm = pid / g.tiles_n, tn = pid % g.tiles_n;
+  const int per_group = GM * g.tiles_n;
+  const int first_m = (pid / per_group) * GM;
+  const int gsz = min(g.tiles_m - first_m, GM);
+  const int tm = first_m + (pid % per_group) % gsz, tn = (pid % per_group) / gsz;
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int kbeg = blockIdx.z * g.k_chunk;
@@ -275,19 +282,19 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ P
 // ------------------------------------------------------------ skinny A@Bᵀ
 // Decode-shaped C[M ≤ 16·MT, N] = X[M, K]·W[N, K]ᵀ (M = sequences decoded
 // together): bound by streaming W once, and too small for the tiled
-// kernel's per-K-step LDS pipeline.  A block owns 16 columns of N and ALL
-// of K; its W waves take 1/W of K each, keep U k-chunks of W and X
-// fragments in flight (X, a few hundred KB, comes from L2) and alternate
-// two accumulator sets so the MFMA dependency chains are half as deep; the
-// W partial tiles are summed through LDS in wave order (deterministic)
-// before the epilogue.  One launch, no inter-block sync.  With gridDim.y > 1
-// the block only covers K range blockIdx.y of gridDim.y and stores its tile
-// to P[blockIdx.y] with no epilogue: the CONSUMER of the product sums the
-// ranges in increasing order (the decode step's LayerNorm does, together
-// with the residual add).
-template <int MT, int W>
+// kernel's per-K-step LDS pipeline.  A block owns 16 columns of N and its
+// K range; in each pass its W waves take W·U consecutive 16-wide k-chunks,
+// U contiguous chunks per wave, all loads issued before the MFMAs (X, a few
+// hundred KB, comes from L2).  The launcher picks U so that the decode
+// shapes need exactly one pass.  Two accumulator sets halve the MFMA
+// dependency chains; the per-wave tiles are summed through LDS in wave
+// order (deterministic) before the epilogue.  One launch, no inter-block
+// sync.  With gridDim.y > 1 the block only covers K range blockIdx.y of
+// gridDim.y and stores its tile to P[blockIdx.y] with no epilogue: the
+// CONSUMER of the product sums the ranges in increasing order (the decode
+// step's LayerNorm does, together with the residual add).
+template <int MT, int W, int U>
 __global__ void __launch_bounds__(64 * W) skinny_nt_kernel(GemmArgs g) {
-  constexpr int U = 8;  // 16-wide k-chunks in flight per wave
   __shared__ float red[W][16 * MT][17];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g16 = lane >> 4, l16 = lane & 15;
@@ -296,19 +303,17 @@ __global__ void __launch_bounds__(64 * W) skinny_nt_kernel(GemmArgs g) {
   const bool nval = n < g.N;
   const int nchunks_all = (g.K + 15) / 16;
   const int cpb = (nchunks_all + gridDim.y - 1) / gridDim.y;  // chunks of this block's K range
-  const int kb = blockIdx.y * cpb, nchunks = min(nchunks_all, kb + cpb);
-  const int per = (cpb + W - 1) / W;
-  const int cb = kb + w * per, ce = min(nchunks, cb + per);
+  const int kb = blockIdx.y * cpb, ke = min(nchunks_all, kb + cpb);
   const float* wrow = g.B + (size_t)(nval ? n : 0) * g.ldb;
   floatx4 acc[MT], acc2[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i] = acc2[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int c0 = cb; c0 < ce; c0 += U) {
+  for (int c0 = kb + w * U; c0 < ke; c0 += W * U) {
     floatx4 wf[U], xf[U][MT];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = 16 * (c0 + u) + 4 * g16;
-      const bool kval = c0 + u < ce && k < g.K;  // K % 4 == 0: a float4 is all in or all out
+      const bool kval = c0 + u < ke && k < g.K;  // K % 4 == 0: a float4 is all in or all out
       floatx4 v = {0.f, 0.f, 0.f, 0.f};
       if (nval && kval) v = *reinterpret_cast<const floatx4*>(wrow + k);
       wf[u] = v;
@@ -321,16 +326,20 @@ __global__ void __launch_bounds__(64 * W) skinny_nt_kernel(GemmArgs g) {
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; u += 2)
+    for (int u = 0; u < U; ++u) {
+      if (c0 + u >= ke) break;  // wave-uniform: no MFMAs on chunks past the range
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
-          acc[i] = mfma16x16x4(xf[u][i][s], wf[u][s], acc[i]);
-          acc2[i] = mfma16x16x4(xf[u + 1][i][s], wf[u + 1][s], acc2[i]);
+          if (u & 1)
+            acc2[i] = mfma16x16x4(xf[u][i][s], wf[u][s], acc2[i]);
+          else
+            acc[i] = mfma16x16x4(xf[u][i][s], wf[u][s], acc[i]);
         }
+    }
   }
-  // acc + acc2 = partial C[16i + 4·g16 + e][n0 + l16] of this wave's K range
+  // acc + acc2 = partial C[16i + 4·g16 + e][n0 + l16] of this wave's chunks
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -443,21 +452,65 @@ static void reduce_partials(aur_ctx* ctx, const float* P, float* C, int M, int N
   hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, P, C, M, N, ldc, splits, epi);
 }
 
+template <int MT, int W>
+static void launch_skinny_u(dim3 grid, int u, const GemmArgs& a, hipStream_t st) {
+  if (u <= 1) {
+    hipLaunchKernelGGL((skinny_nt_kernel<MT, W, 1>), grid, dim3(64 * W), 0, st, a);
+  } else if (u == 2) {
+    hipLaunchKernelGGL((skinny_nt_kernel<MT, W, 2>), grid, dim3(64 * W), 0, st, a);
+  } else if constexpr (MT == 4 || W == 16) {  // register budget: at most 4 chunks in flight
+    hipLaunchKernelGGL((skinny_nt_kernel<MT, W, 4>), grid, dim3(64 * W), 0, st, a);
+  } else {
+    if (u <= 4)
+      hipLaunchKernelGGL((skinny_nt_kernel<MT, W, 4>), grid, dim3(64 * W), 0, st, a);
+    else
+      hipLaunchKernelGGL((skinny_nt_kernel<MT, W, 8>), grid, dim3(64 * W), 0, st, a);
+  }
+}
+
 // Decode-shaped A@Bᵀ (M ≤ 64, both operands k-contiguous, 16-byte vectors).
 // splits > 1: K ranges write P[splits][M][N] instead of C (no epilogue).
+// Waves per block W and chunks per wave U: the block's K range in one pass
+// (W·U ≥ its 16-wide chunks) with as few chunks per wave as that allows;
+// more than one block per CU's worth of columns (the tied head) prefers
+// W = 8, so two blocks share a CU.  AUR_SKINNY_CFG="W:U" overrides (tuning).
 static int skinny_nt(aur_ctx* ctx, const float* A, int lda, const float* B, int ldb, float* C, int ldc,
                      int M, int N, int K, const Epilogue& epi, float* P = nullptr, int splits = 1) {
   GemmArgs a{};
   a.A = A; a.B = B; a.C = C; a.M = M; a.N = N; a.K = K;
   a.lda = lda; a.ldb = ldb; a.ldc = ldc; a.epi = epi; a.P = P;
-  // 16 waves per block (K split 16 ways) while the registers allow it.
+  const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  const int blocks = (N + 15) / 16 * splits;
+  const int nck = ((K + 15) / 16 + splits - 1) / splits;  // chunks per block
+  int w = (mt == 4 || blocks > cus) ? 8 : 16;
+  int u = 1;
+  while (u < 8 && w * u < nck) u *= 2;
+  if (mt == 4 && u > 4) u = 4;
+  if (mt < 4 && w == 16 && u > 4) u = 4;
+  if (const char* env = std::getenv("AUR_SKINNY_CFG")) {
+    int ew = 0, eu = 0;
+    if (std::sscanf(env, "%d:%d", &ew, &eu) == 2 && (ew == 4 || ew == 8 || ew == 16) &&
+        (eu == 1 || eu == 2 || eu == 4 || eu == 8) && !(mt == 4 && (ew == 16 || eu == 8)) &&
+        !(ew == 16 && eu == 8)) {
+      w = ew;
+      u = eu;
+    }
+  }
   dim3 grid((N + 15) / 16, splits);
-  if (M <= 16)
-    hipLaunchKernelGGL((skinny_nt_kernel<1, 16>), grid, dim3(1024), 0, ctx->stream, a);
-  else if (M <= 32)
-    hipLaunchKernelGGL((skinny_nt_kernel<2, 16>), grid, dim3(1024), 0, ctx->stream, a);
-  else
-    hipLaunchKernelGGL((skinny_nt_kernel<4, 8>), grid, dim3(512), 0, ctx->stream, a);
+  hipStream_t st = ctx->stream;
+  if (mt == 1) {
+    if (w == 16) launch_skinny_u<1, 16>(grid, u, a, st);
+    else if (w == 8) launch_skinny_u<1, 8>(grid, u, a, st);
+    else launch_skinny_u<1, 4>(grid, u, a, st);
+  } else if (mt == 2) {
+    if (w == 16) launch_skinny_u<2, 16>(grid, u, a, st);
+    else if (w == 8) launch_skinny_u<2, 8>(grid, u, a, st);
+    else launch_skinny_u<2, 4>(grid, u, a, st);
+  } else {
+    if (w == 8) launch_skinny_u<4, 8>(grid, u, a, st);
+    else launch_skinny_u<4, 4>(grid, u, a, st);
+  }
   AUR_LAUNCH_CHECK(ctx, "skinny_nt_kernel");
   return 0;
 }

@@ -28,6 +28,7 @@ import numpy as np
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 PEAK_HBM = 8000.0       # GB/s
 
+COPY_MIB = 256          # calibration copy of the --only traffic leg
 SWEEP_KN = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
 M = 8192
 
@@ -245,7 +246,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["head", "sweep", "train", "decode", "attention"], default=None,
+    ap.add_argument("--only", choices=["head", "sweep", "train", "decode", "attention", "traffic"],
+                    default=None,
                     help="profile helper: time only this part and skip the CPU baseline")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -270,6 +272,20 @@ def main() -> int:
             head[2]()
         ms = time_region(ctx, head[2], args.steps)
         log(f"[bench] head gemm {ms:.4f} ms  {head[1] / ms / 1e9:.1f} TFLOP/s")
+        return 0
+    if args.only == "traffic":
+        # For `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` passes: the head GEMM,
+        # then a device copy of COPY_MIB as the counters' calibration (its
+        # algorithmic bytes are known: COPY_MIB read + COPY_MIB written).
+        from aurora_amd.gpu import GpuBuffer
+        src = GpuBuffer.zeros(ctx, COPY_MIB << 18)
+        dst = GpuBuffer.empty(ctx, COPY_MIB << 18)
+        for _ in range(max(1, args.steps)):
+            head[2]()
+        for _ in range(max(1, args.steps)):
+            ctx.call("aur_d2d", dst.ptr, src.ptr, COPY_MIB << 20)
+        ctx.sync()
+        log(f"[bench] traffic leg: {args.steps} head GEMMs, {args.steps} copies of {COPY_MIB} MiB")
         return 0
     if args.only == "train":
         bench_train(ctx, max(1, args.steps), args.warmup)
