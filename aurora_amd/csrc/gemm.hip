@@ -364,27 +364,37 @@ struct Plan {
 
 constexpr int kBK = 32;
 
+// Launch plan: tile shape and split-K count.  A CU holds two 128×128 or
+// 128×64 blocks (LDS) or four 64×64 ones, so a launch runs in "waves" of
+// CUs × occupancy blocks and a partly filled last wave idles the rest of
+// the chip.  Each candidate (tile, splits) is scored by its wave
+// quantisation efficiency times the tile's measured relative MFMA
+// efficiency on MI355X (128×128: 1.00, 128×64: 0.90, 64×64: 0.88) times a
+// 0.97 penalty for the split-K reduction; splits keep ≥ 512 of K per block.
+// The highest score wins, ties going to the larger tile and fewer splits.
 Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split) {
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-  auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  struct Cand {
+    int bm, bn, occ;
+    double eff;
+  };
+  static constexpr Cand cands[] = {{128, 128, 2, 1.00}, {128, 64, 2, 0.90}, {64, 64, 4, 0.88}};
   Plan p{128, 128, 1, K};
-  if (tiles(128, 128) >= cus) {
-    p = {128, 128, 1, K};
-  } else if (tiles(128, 64) >= cus) {
-    p = {128, 64, 1, K};
-  } else {
-    p = {64, 64, 1, K};
-    if (tiles(128, 128) * 4 >= cus && K >= 2048) p = {128, 128, 1, K};
-  }
-  if (allow_split) {
-    const int t = tiles(p.bm, p.bn);
-    int splits = 1;
-    while (t * splits < cus && K / (splits * 2) >= 256) splits *= 2;
-    if (splits > 1) {
-      int chunk = (K + splits - 1) / splits;
-      chunk = (chunk + kBK - 1) / kBK * kBK;
-      p.splits = (K + chunk - 1) / chunk;
-      p.k_chunk = chunk;
+  double best = -1.0;
+  for (const Cand& c : cands) {
+    const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const long slots = (long)cus * c.occ;
+    for (int s = 1; s <= 16; s *= 2) {
+      if (s > 1 && (!allow_split || K / s < 512)) break;
+      const long blocks = tiles * s;
+      const long waves = (blocks + slots - 1) / slots;
+      const double score = (double)blocks / (double)(waves * slots) * c.eff * (s > 1 ? 0.97 : 1.0);
+      if (score > best + 1e-9) {
+        best = score;
+        int chunk = (K + s - 1) / s;
+        chunk = (chunk + kBK - 1) / kBK * kBK;
+        p = {c.bm, c.bn, (K + chunk - 1) / chunk, chunk};
+      }
     }
   }
   // Tuning override: AUR_GEMM_CFG="BMxBN[:splits]".
