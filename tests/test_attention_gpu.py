@@ -193,3 +193,42 @@ def test_kv_step_batched_ragged_lengths(ctx):
         want = oracle.kv_attend(q_new[i * d:(i + 1) * d], kh[i * max_len * d:(i + 1) * max_len * d],
                                 vh[i * max_len * d:(i + 1) * max_len * d], int(lens[i]), H, dh)
         assert fro_rel(got[i], want) < TOL_ATTN, i
+
+
+@pytest.mark.parametrize("dh", [8, 16, 32, 64])
+def test_kv_step_batched_one_block_per_head(ctx, dh, monkeypatch):
+    """B·H ≥ CU count takes the single-launch path (a block per sequence and
+    head, waves merged in LDS).  Ragged lengths including 1 and max_len,
+    against the oracle per sequence, against the chunked two-launch path,
+    and bit-identical on a repeat."""
+    from aurora_amd.gpu import GpuBuffer, MhaKvCacheKernel
+
+    B, max_len = 32, 700
+    H = 256 // B * (2 if dh <= 16 else 1)
+    d = H * dh
+    rng = np.random.default_rng(41 + dh)
+    lens = rng.integers(1, max_len + 1, B).astype(np.int32)
+    lens[0], lens[1], lens[2] = 1, max_len, 2
+    t_max = int(lens.max())
+    q_new = _n(rng, B * d)
+    kh, vh = _n(rng, B * max_len * d), _n(rng, B * max_len * d)
+    bq, bk, bv = (GpuBuffer.from_slice(ctx, x) for x in (q_new, kh, vh))
+    bt = GpuBuffer.from_slice(ctx, lens)
+    scratch = GpuBuffer.empty(ctx, MhaKvCacheKernel.scratch_len(H, max_len, B))
+    kern = MhaKvCacheKernel.new(ctx)
+
+    def run():
+        out = GpuBuffer.zeros(ctx, B * d)
+        kern.dispatch_batched(ctx, bq, bk, bv, out, scratch, bt, t_max, B, H, dh, max_len)
+        return out.download().reshape(B, d)
+
+    got = run()
+    np.testing.assert_array_equal(run(), got)
+    for i in range(B):
+        want = oracle.kv_attend(q_new[i * d:(i + 1) * d], kh[i * max_len * d:(i + 1) * max_len * d],
+                                vh[i * max_len * d:(i + 1) * max_len * d], int(lens[i]), H, dh)
+        assert fro_rel(got[i], want) < TOL_ATTN, i
+        assert max_rel_err(got[i], want) < TOL_REF, i
+    monkeypatch.setenv("AUR_KV_CHUNKED", "1")
+    chunked = run()
+    assert fro_rel(got, chunked) < 1e-5
