@@ -5,6 +5,7 @@ Loading fails loudly: there is no CPU fallback for any entry point.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libaurora_hip.so"
@@ -91,11 +92,13 @@ def load() -> C.CDLL:
     global _lib
     if _lib is not None:
         return _lib
-    if not LIB_PATH.exists():
+    # AUR_LIB: another build of the same library (A/B timing of two builds).
+    path = Path(os.environ["AUR_LIB"]) if os.environ.get("AUR_LIB") else LIB_PATH
+    if not path.exists():
         raise ImportError(
-            f"{LIB_PATH} is missing: build it first (python -c "
+            f"{path} is missing: build it first (python -c "
             "'import __graft_entry__ as g; g.build()'); there is no CPU fallback")
-    lib = C.CDLL(str(LIB_PATH))
+    lib = C.CDLL(str(path))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res

@@ -60,8 +60,11 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
          const Workspace* ws = nullptr);
 int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
          int ldb, float* C, int ldc, int M, int N, int K, bool accumulate);
-// Decode-shaped A@Bᵀ (M ≤ 64) split into `splits` K ranges whose products
-// are stored to P[splits][M][N] for the consumer to sum in range order.
+// Decode-shaped A@Bᵀ (M ≤ 64) split into `splits` K ranges (each a multiple
+// of 64 long, none empty) whose products are stored to P[splits][M][N] for
+// the consumer to sum in range order.  gemm_nt_partials_splits gives the
+// split count that keeps about one block per CU in flight.
+int gemm_nt_partials_splits(int M, int N, int K);
 int gemm_nt_partials(aur_ctx* ctx, const float* A, int lda, const float* B, int ldb, float* P, int M, int N,
                      int K, int splits);
 

@@ -291,52 +291,76 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ P
 // order (deterministic) before the epilogue.  One launch, no inter-block
 // sync.  With gridDim.y > 1 the block only covers K range blockIdx.y of
 // gridDim.y and stores its tile to P[blockIdx.y] with no epilogue: the
-// CONSUMER of the product sums the ranges in increasing order (the decode
-// step's LayerNorm does, together with the residual add).
+// CONSUMER of the product sums the ranges in increasing order.
+//
+// Loads are coalesced: lanes 4r..4r+3 read row r's 64 contiguous bytes of a
+// 16-row × 16-k chunk (in the MFMA operand layout neighbouring lanes would
+// read different rows, one 16-byte L1 access per lane — measured 2× slower
+// at the decode shapes).  One ds_bpermute per component then moves the
+// chunk into the MFMA layout (lane 16g+m holds row m, k offset 4g).
+__device__ __forceinline__ floatx4 to_mfma_layout(floatx4 v, int addr) {
+  floatx4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(v[e])));
+  return r;
+}
+
 template <int MT, int W, int U>
 __global__ void __launch_bounds__(64 * W) skinny_nt_kernel(GemmArgs g) {
   __shared__ float red[W][16 * MT][17];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g16 = lane >> 4, l16 = lane & 15;
+  const int lr = lane >> 2, lk = (lane & 3) * 4;       // load mapping: row lr, k offset lk
+  const int perm = 4 * (4 * l16 + g16);                // bpermute byte address of the source lane
   const int n0 = blockIdx.x * 16;
-  const int n = n0 + l16;
-  const bool nval = n < g.N;
+  const bool wrow_ok = n0 + lr < g.N;
   const int nchunks_all = (g.K + 15) / 16;
   const int cpb = (nchunks_all + gridDim.y - 1) / gridDim.y;  // chunks of this block's K range
   const int kb = blockIdx.y * cpb, ke = min(nchunks_all, kb + cpb);
-  const float* wrow = g.B + (size_t)(nval ? n : 0) * g.ldb;
+  const float* wrow = g.B + (size_t)(wrow_ok ? n0 + lr : 0) * g.ldb;
   floatx4 acc[MT], acc2[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i] = acc2[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   for (int c0 = kb + w * U; c0 < ke; c0 += W * U) {
+    // Branch-free loads: an out-of-range row or k is clamped to an in-bounds
+    // address and its value replaced by 0 after the scheduling barrier, so
+    // every load of the pass is issued first and each MFMA waits only for
+    // its own operands.  A chunk past the range is all zeros and adds
+    // nothing: no branch between the loads and the math.
     floatx4 wf[U], xf[U][MT];
+    bool kv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = 16 * (c0 + u) + 4 * g16;
-      const bool kval = c0 + u < ke && k < g.K;  // K % 4 == 0: a float4 is all in or all out
-      floatx4 v = {0.f, 0.f, 0.f, 0.f};
-      if (nval && kval) v = *reinterpret_cast<const floatx4*>(wrow + k);
-      wf[u] = v;
+      const int k = 16 * (c0 + u) + lk;
+      kv[u] = c0 + u < ke && k < g.K;  // K % 4 == 0: a float4 is all in or all out
+      const int kc = kv[u] ? k : 0;
+      wf[u] = *reinterpret_cast<const floatx4*>(wrow + kc);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        const int r = 16 * i + l16;
-        floatx4 x = {0.f, 0.f, 0.f, 0.f};
-        if (kval && r < g.M) x = *reinterpret_cast<const floatx4*>(g.A + (size_t)r * g.lda + k);
-        xf[u][i] = x;
+        const int r = 16 * i + lr;
+        xf[u][i] = *reinterpret_cast<const floatx4*>(g.A + (size_t)(r < g.M ? r : 0) * g.lda + kc);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (c0 + u >= ke) break;  // wave-uniform: no MFMAs on chunks past the range
+      const bool wv = wrow_ok && kv[u];
+      const floatx4 wz = to_mfma_layout(
+          floatx4{wv ? wf[u][0] : 0.f, wv ? wf[u][1] : 0.f, wv ? wf[u][2] : 0.f, wv ? wf[u][3] : 0.f}, perm);
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int i = 0; i < MT; ++i) {
+        const bool xv = kv[u] && 16 * i + lr < g.M;
+        const floatx4 xz = to_mfma_layout(floatx4{xv ? xf[u][i][0] : 0.f, xv ? xf[u][i][1] : 0.f,
+                                                  xv ? xf[u][i][2] : 0.f, xv ? xf[u][i][3] : 0.f},
+                                          perm);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
+        for (int s = 0; s < 4; ++s) {
           if (u & 1)
-            acc2[i] = mfma16x16x4(xf[u][i][s], wf[u][s], acc2[i]);
+            acc2[i] = mfma16x16x4(xz[s], wz[s], acc2[i]);
           else
-            acc[i] = mfma16x16x4(xf[u][i][s], wf[u][s], acc[i]);
+            acc[i] = mfma16x16x4(xz[s], wz[s], acc[i]);
         }
+      }
     }
   }
   // acc + acc2 = partial C[16i + 4·g16 + e][n0 + l16] of this wave's chunks
@@ -355,6 +379,98 @@ __global__ void __launch_bounds__(64 * W) skinny_nt_kernel(GemmArgs g) {
       g.P[((size_t)blockIdx.y * g.M + row) * g.N + n0 + col] = v;
     else
       apply_epilogue(g.epi, g.C, (size_t)row * g.ldc + n0 + col, v);
+  }
+}
+
+// ------------------------------------------------ decode K-range partials
+// P[z][M ≤ 16·MT][N] = X[M, K_z]·W[N, K_z]ᵀ for K range z = blockIdx.y of
+// length k_chunk.  A 256-thread block owns 64 columns and one K range; its X
+// and W slices go through LDS 64 k at a time with coalesced float4 loads (a
+// wave load instruction reads four 256-byte row pieces), the next slice
+// prefetched into registers while the current one is multiplied; wave w
+// multiplies columns 16w..16w+15.  Against the 16-column skinny kernel,
+// every X byte staged here serves 4× more W bytes, and the K ranges keep
+// about one block per CU in flight even for N = d_model.  No epilogue:
+// the consumer sums the ranges in increasing order.
+template <int MT>
+__global__ void __launch_bounds__(256) wide_partials_kernel(GemmArgs g) {
+  constexpr int SUB = 64, LD = SUB + 4, XR = 16 * MT;
+  constexpr int XPT = XR * SUB / 4 / 256, WPT = 64 * SUB / 4 / 256;  // float4 per thread
+  __shared__ __attribute__((aligned(16))) float xs[XR * LD];
+  __shared__ __attribute__((aligned(16))) float ws[64 * LD];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int g16 = lane >> 4, l16 = lane & 15;
+  const int n0 = blockIdx.x * 64;
+  const int kb = blockIdx.y * g.k_chunk, ke = min(g.K, kb + g.k_chunk);
+  floatx4 xr[XPT], wr[WPT];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+      const int f = tid + 256 * i, r = f / (SUB / 4), k = k0 + (f % (SUB / 4)) * 4;
+      floatx4 v = {0.f, 0.f, 0.f, 0.f};
+      if (n0 + r < g.N && k < ke) v = *reinterpret_cast<const floatx4*>(g.B + (size_t)(n0 + r) * g.ldb + k);
+      wr[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int f = tid + 256 * i, r = f / (SUB / 4), k = k0 + (f % (SUB / 4)) * 4;
+      floatx4 v = {0.f, 0.f, 0.f, 0.f};
+      if (r < g.M && k < ke) v = *reinterpret_cast<const floatx4*>(g.A + (size_t)r * g.lda + k);
+      xr[i] = v;
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+      const int f = tid + 256 * i;
+      *reinterpret_cast<floatx4*>(ws + (f / (SUB / 4)) * LD + (f % (SUB / 4)) * 4) = wr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int f = tid + 256 * i;
+      *reinterpret_cast<floatx4*>(xs + (f / (SUB / 4)) * LD + (f % (SUB / 4)) * 4) = xr[i];
+    }
+  };
+  floatx4 acc[MT], acc2[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = acc2[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  load(kb);
+  store();
+  __syncthreads();
+  for (int k0 = kb; k0 < ke; k0 += SUB) {
+    const bool more = k0 + SUB < ke;
+    if (more) load(k0 + SUB);
+#pragma unroll
+    for (int u = 0; u < SUB / 16; ++u) {
+      const int k = 16 * u + 4 * g16;
+      const floatx4 wf = *reinterpret_cast<const floatx4*>(ws + (16 * wv + l16) * LD + k);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const floatx4 xf = *reinterpret_cast<const floatx4*>(xs + (16 * i + l16) * LD + k);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          if (u & 1)
+            acc2[i] = mfma16x16x4(xf[s], wf[s], acc2[i]);
+          else
+            acc[i] = mfma16x16x4(xf[s], wf[s], acc[i]);
+        }
+      }
+    }
+    if (more) {
+      __syncthreads();  // every wave is done with the slice
+      store();
+      __syncthreads();
+    }
+  }
+  const int col = n0 + 16 * wv + l16;
+  if (col < g.N) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * i + 4 * g16 + e;
+        if (row < g.M) g.P[((size_t)blockIdx.y * g.M + row) * g.N + col] = acc[i][e] + acc2[i][e];
+      }
   }
 }
 
@@ -594,12 +710,36 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
   return gemm(ctx, a_kcontig, b_kcontig, A, lda, B, ldb, C, ldc, M, N, K, e, nullptr);
 }
 
+int gemm_nt_partials_splits(int M, int N, int K) {
+  (void)M;
+  const int groups = (N + 63) / 64;
+  int s = 1;
+  while (groups * s < 256 && K / (2 * s) >= 64) s *= 2;
+  return s;
+}
+
 int gemm_nt_partials(aur_ctx* ctx, const float* A, int lda, const float* B, int ldb, float* P, int M, int N,
                      int K, int splits) {
-  if (M < 1 || M > 64 || N < 1 || K < 16 * splits || splits < 1 || (K & 3) || (lda & 3) || (ldb & 3) ||
+  if (M < 1 || M > 64 || N < 1 || K < 1 || splits < 1 || (K & 3) || (lda & 3) || (ldb & 3) ||
       !aligned16(A) || !aligned16(B) || !P)
     return set_error(ctx, AUR_EINVAL, "gemm_nt_partials: unsupported shape or alignment");
-  return skinny_nt(ctx, A, lda, B, ldb, nullptr, 0, M, N, K, Epilogue{}, P, splits);
+  // K ranges of a multiple of 64; every one of the `splits` ranges non-empty.
+  int chunk = (K + splits - 1) / splits;
+  chunk = (chunk + 63) / 64 * 64;
+  if ((K + chunk - 1) / chunk != splits)
+    return set_error(ctx, AUR_EINVAL, "gemm_nt_partials: %d K ranges do not fit K=%d", splits, K);
+  GemmArgs a{};
+  a.A = A; a.B = B; a.P = P; a.M = M; a.N = N; a.K = K;
+  a.lda = lda; a.ldb = ldb; a.k_chunk = chunk;
+  dim3 grid((N + 63) / 64, splits);
+  if (M <= 16)
+    hipLaunchKernelGGL(wide_partials_kernel<1>, grid, dim3(256), 0, ctx->stream, a);
+  else if (M <= 32)
+    hipLaunchKernelGGL(wide_partials_kernel<2>, grid, dim3(256), 0, ctx->stream, a);
+  else
+    hipLaunchKernelGGL(wide_partials_kernel<4>, grid, dim3(256), 0, ctx->stream, a);
+  AUR_LAUNCH_CHECK(ctx, "wide_partials_kernel");
+  return 0;
 }
 
 }  // namespace aur

@@ -174,7 +174,10 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
 // One block of SW waves per (head, sequence).  Round r covers keys
 // [r·SW·U·KPS, (r+1)·SW·U·KPS); wave w loads its U key groups of the round
 // (KPS keys per load instruction, LPK lanes per key) and folds them into its
-// running (m, l, acc) in the log2 domain.
+// running (m, l, acc) in the log2 domain.  The loads are branch-free (a key
+// past the end is clamped to the last one and masked in the math) and the
+// next round is loaded before the current one is used, so each wave keeps
+// two rounds of HBM reads in flight instead of one round trip per round.
 constexpr int SW = 8;  // waves per block
 template <int DH, int U>
 __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
@@ -188,36 +191,42 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
   const int T = min(a.t_dev ? a.t_dev[b] : a.t_scalar, t_max);
   const size_t hist = (size_t)b * a.max_len;
   const size_t col = (size_t)h * DH + 4 * part;
+  const float* krow_new = a.knew ? a.knew + (size_t)b * a.ld_q + col : nullptr;
+  const float* vrow_new = a.vnew ? a.vnew + (size_t)b * a.ld_q + col : nullptr;
+  // Fused append: the new row (position T-1) goes into the history; the
+  // attention below reads it from knew/vnew, so this store has no reader.
+  if (a.knew && T >= 1 && w == 0 && g == 0) {
+    *reinterpret_cast<floatx4*>(const_cast<float*>(a.kh) + (hist + T - 1) * a.ld + col) =
+        *reinterpret_cast<const floatx4*>(krow_new);
+    *reinterpret_cast<floatx4*>(const_cast<float*>(a.vh) + (hist + T - 1) * a.ld + col) =
+        *reinterpret_cast<const floatx4*>(vrow_new);
+  }
   floatx4 qv = *reinterpret_cast<const floatx4*>(a.q + (size_t)b * a.ld_q + col);
   qv *= a.scale * LOG2E;
-  float m = -INFINITY, l = 0.f;
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int base = 0; base < T; base += ROUND) {
-    floatx4 kr[U], vr[U];
+  const int last = max(T - 1, 0);
+  auto load = [&](int base, floatx4* kr, floatx4* vr) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int key = base + (u * SW + w) * KPS + g;
-      floatx4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-      if (key < T) {
-        if (a.knew && key == T - 1) {
-          const size_t o = (size_t)b * a.ld_q + col;
-          kv = *reinterpret_cast<const floatx4*>(a.knew + o);
-          vv = *reinterpret_cast<const floatx4*>(a.vnew + o);
-          *reinterpret_cast<floatx4*>(const_cast<float*>(a.kh) + (hist + key) * a.ld + col) = kv;
-          *reinterpret_cast<floatx4*>(const_cast<float*>(a.vh) + (hist + key) * a.ld + col) = vv;
-        } else {
-          kv = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + col);
-          vv = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + col);
-        }
-      }
-      kr[u] = kv;
-      vr[u] = vv;
+      const int key = min(base + (u * SW + w) * KPS + g, last);
+      const bool is_new = a.knew != nullptr && key == T - 1;
+      const float* kp = is_new ? krow_new : a.kh + (hist + key) * a.ld + col;
+      const float* vp = is_new ? vrow_new : a.vh + (hist + key) * a.ld + col;
+      kr[u] = *reinterpret_cast<const floatx4*>(kp);
+      vr[u] = *reinterpret_cast<const floatx4*>(vp);
     }
+  };
+  float m = -INFINITY, l = 0.f;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  floatx4 kc[U], vc[U];
+  load(0, kc, vc);
+  for (int base = 0; base < T; base += ROUND) {
+    floatx4 kn[U], vn[U];
+    load(base + ROUND, kn, vn);  // clamped: past the end it re-reads the last row (cached)
     float sc[U];
     float mx = -INFINITY;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      float s = qv[0] * kr[u][0] + qv[1] * kr[u][1] + qv[2] * kr[u][2] + qv[3] * kr[u][3];
+      float s = qv[0] * kc[u][0] + qv[1] * kc[u][1] + qv[2] * kc[u][2] + qv[3] * kc[u][3];
 #pragma unroll
       for (int o = LPK / 2; o >= 1; o >>= 1) s += shfl_xor(s, o);
       if (base + (u * SW + w) * KPS + g >= T) s = -INFINITY;
@@ -227,17 +236,23 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
 #pragma unroll
     for (int o = LPK; o < 64; o <<= 1) mx = fmaxf(mx, shfl_xor(mx, o));
     const float m_new = fmaxf(m, mx);
-    if (m_new == -INFINITY) continue;  // wave-uniform: no key of this wave so far
-    const float alpha = exp2f(m - m_new);
-    l *= alpha;
-    acc *= alpha;
+    if (m_new != -INFINITY) {  // wave-uniform: some key of this wave so far
+      const float alpha = exp2f(m - m_new);
+      l *= alpha;
+      acc *= alpha;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float p = exp2f(sc[u] - m_new);  // 0 for keys past T
+        l += p;
+        acc += p * vc[u];
+      }
+      m = m_new;
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float p = exp2f(sc[u] - m_new);  // 0 for keys past T
-      l += p;
-      acc += p * vr[u];
+      kc[u] = kn[u];
+      vc[u] = vn[u];
     }
-    m = m_new;
   }
   // Sum the lane groups (each group holds its own keys' l and acc).
 #pragma unroll

@@ -441,8 +441,10 @@ KvCacheGpu::KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch_, uint
   const size_t B = batch, d = d_model, F = c.d_ff, V = c.vocab;
   const size_t hist = (size_t)n_layer * B * max_len * d;
   const size_t scratch = (aur_mha_kv_ws_bytes(batch, c.n_head, max_len) + 3) / 4;
-  // K-range partial products of the W_o / W_proj decode GEMMs: ≤ 4 × [B, d].
-  part_floats_ = 4 * B * d;
+  // K-range partial products of the W_o / W_proj decode GEMMs: [splits][B][d].
+  part_floats_ = (size_t)std::max(aur::gemm_nt_partials_splits((int)B, (int)d, (int)d),
+                                  aur::gemm_nt_partials_splits((int)B, (int)d, (int)F)) *
+                 B * d;
   // x, ln, qkv (3), attn, xmid = 7 rows of d per sequence
   const size_t floats = 2 * hist + B * (d * 7 + 2 * F + V) + scratch + part_floats_;
   bytes_ = floats * 4 + 3 * B * 4 + 32 * 256;
@@ -552,12 +554,13 @@ void DecoderTransformerGpu::encode_decode_step(KvCacheGpu& cache) {
   // following LayerNorm sums (with the residual add) — more blocks in flight
   // and no separate reduction launch.
   const bool split = cache.batch <= 64;
-  const int s_o = std::max(1, std::min(4, d / 16)), s_p = std::max(1, std::min(4, F / 16));
+  const int s_o = aur::gemm_nt_partials_splits(B, d, d), s_p = aur::gemm_nt_partials_splits(B, d, F);
   // h = w_tok[tok] + w_pos[pos]  (kv_cache.rs:103-115)
   ck(ctx_, aur::embed_forward(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, 0, cache.x_, B, d), "embed");
   ck(ctx_, aur::lens_from_pos(ctx_, cache.pos_, cache.lens_, B), "lens");
-  // Every chunk up to max_len is launched; chunks past a sequence's length
-  // exit at once, so the launch shape is the same for every step.
+  // Attention is launched for lengths up to max_len (keys past a sequence's
+  // length are skipped on the device), so the launch shape is the same for
+  // every step.
   const int t_max = (int)cache.max_len;
   for (uint32_t l = 0; l < cfg_.n_layer; ++l) {
     Layer& Y = (*layers_)[l];

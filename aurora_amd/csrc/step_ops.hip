@@ -183,8 +183,18 @@ __global__ void __launch_bounds__(256) ln_fwd_sum_kernel(const float* __restrict
     const int c = (threadIdx.x + 256 * i) * 4;
     floatx4 v = {0.f, 0.f, 0.f, 0.f};
     if (c < d) {
-      floatx4 acc = *reinterpret_cast<const floatx4*>(P + (size_t)r * d + c);
-      for (int z = 1; z < np; ++z) acc += *reinterpret_cast<const floatx4*>(P + z * pstride + (size_t)r * d + c);
+      // Partials summed in z order; loaded 8 at a time so their latencies overlap.
+      const float* pc = P + (size_t)r * d + c;
+      floatx4 acc = *reinterpret_cast<const floatx4*>(pc);
+      int z = 1;
+      for (; z + 8 <= np; z += 8) {
+        floatx4 t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = *reinterpret_cast<const floatx4*>(pc + (size_t)(z + j) * pstride);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += t[j];
+      }
+      for (; z < np; ++z) acc += *reinterpret_cast<const floatx4*>(pc + (size_t)z * pstride);
       v = *reinterpret_cast<const floatx4*>(R + (size_t)r * d + c) + acc;
       *reinterpret_cast<floatx4*>(xo + (size_t)r * d + c) = v;
       s += (v[0] + v[1]) + (v[2] + v[3]);
