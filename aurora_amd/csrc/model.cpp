@@ -556,8 +556,9 @@ void DecoderTransformerGpu::encode_decode_step(KvCacheGpu& cache) {
   const bool split = cache.batch <= 64;
   const int s_o = aur::gemm_nt_partials_splits(B, d, d), s_p = aur::gemm_nt_partials_splits(B, d, F);
   // h = w_tok[tok] + w_pos[pos]  (kv_cache.rs:103-115)
-  ck(ctx_, aur::embed_forward(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, 0, cache.x_, B, d), "embed");
-  ck(ctx_, aur::lens_from_pos(ctx_, cache.pos_, cache.lens_, B), "lens");
+  // (and lens = pos + 1 for the attention below)
+  ck(ctx_, aur::embed_forward(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, 0, cache.x_, B, d, cache.lens_),
+     "embed");
   // Attention is launched for lengths up to max_len (keys past a sequence's
   // length are skipped on the device), so the launch shape is the same for
   // every step.

@@ -51,10 +51,12 @@ __global__ void __launch_bounds__(256) embed_fwd_kernel(const float* __restrict_
                                                         const float* __restrict__ w_pos,
                                                         const uint32_t* __restrict__ tok,
                                                         const int32_t* __restrict__ pos_dev, int T,
-                                                        float* __restrict__ out, int rows, int d) {
+                                                        float* __restrict__ out, int rows, int d,
+                                                        int32_t* __restrict__ lens) {
   const int r = blockIdx.x;
   if (r >= rows) return;
   const int p = pos_dev ? pos_dev[r] : r % T;
+  if (lens && threadIdx.x == 0) lens[r] = p + 1;  // decode: attention length incl. this token
   const float* a = w_tok + (size_t)tok[r] * d;
   const float* b = w_pos + (size_t)p * d;
   float* o = out + (size_t)r * d;
@@ -183,19 +185,22 @@ __global__ void __launch_bounds__(256) ln_fwd_sum_kernel(const float* __restrict
     const int c = (threadIdx.x + 256 * i) * 4;
     floatx4 v = {0.f, 0.f, 0.f, 0.f};
     if (c < d) {
-      // Partials summed in z order; loaded 8 at a time so their latencies overlap.
+      // Partials summed in z order.  16 at a time, branch-free (an index
+      // past np re-reads the last partial and adds 0), so all of a batch's
+      // loads are in flight together — one memory round trip for np ≤ 16.
       const float* pc = P + (size_t)r * d + c;
-      floatx4 acc = *reinterpret_cast<const floatx4*>(pc);
-      int z = 1;
-      for (; z + 8 <= np; z += 8) {
-        floatx4 t[8];
+      const floatx4 rv = *reinterpret_cast<const floatx4*>(R + (size_t)r * d + c);
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int z0 = 0; z0 < np; z0 += 16) {
+        floatx4 t[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) t[j] = *reinterpret_cast<const floatx4*>(pc + (size_t)(z + j) * pstride);
+        for (int j = 0; j < 16; ++j)
+          t[j] = *reinterpret_cast<const floatx4*>(pc + (size_t)min(z0 + j, np - 1) * pstride);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc += t[j];
+        for (int j = 0; j < 16; ++j)
+          if (z0 + j < np) acc += t[j];
       }
-      for (; z < np; ++z) acc += *reinterpret_cast<const floatx4*>(pc + (size_t)z * pstride);
-      v = *reinterpret_cast<const floatx4*>(R + (size_t)r * d + c) + acc;
+      v = rv + acc;
       *reinterpret_cast<floatx4*>(xo + (size_t)r * d + c) = v;
       s += (v[0] + v[1]) + (v[2] + v[3]);
     }
@@ -416,12 +421,6 @@ __global__ void __launch_bounds__(256) kv_store_kernel(const float* __restrict__
   }
 }
 
-// lens[b] = pos[b] + 1 (attention length after appending position pos[b]).
-__global__ void lens_from_pos_kernel(const int32_t* __restrict__ pos, int32_t* __restrict__ lens, int B) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b < B) lens[b] = pos[b] + 1;
-}
-
 // First index of the row maximum (src/transformer/loss.rs argmax: strict >).
 // pos (optional): the row's sequence position is advanced by one — the end
 // of a decode step.
@@ -478,9 +477,9 @@ namespace aur {
 #define LAUNCH_OK(ctx, name) AUR_LAUNCH_CHECK(ctx, name); return 0
 
 int embed_forward(aur_ctx* ctx, const float* w_tok, const float* w_pos, const uint32_t* tok,
-                  const int32_t* pos_dev, int T, float* out, int rows, int d) {
+                  const int32_t* pos_dev, int T, float* out, int rows, int d, int32_t* lens) {
   hipLaunchKernelGGL(embed_fwd_kernel, dim3(rows), dim3(256), 0, ctx->stream, w_tok, w_pos, tok, pos_dev,
-                     T, out, rows, d);
+                     T, out, rows, d, lens);
   LAUNCH_OK(ctx, "embed_fwd_kernel");
 }
 
@@ -571,11 +570,6 @@ int kv_store(aur_ctx* ctx, const float* qkv, int d, float* kh, float* vh, int ma
   hipLaunchKernelGGL(kv_store_kernel, dim3(rows), dim3(256), 0, ctx->stream, qkv, d, kh, vh, max_len,
                      pos_dev, T);
   LAUNCH_OK(ctx, "kv_store_kernel");
-}
-
-int lens_from_pos(aur_ctx* ctx, const int32_t* pos, int32_t* lens, int B) {
-  hipLaunchKernelGGL(lens_from_pos_kernel, dim3((B + 255) / 256), dim3(256), 0, ctx->stream, pos, lens, B);
-  LAUNCH_OK(ctx, "lens_from_pos_kernel");
 }
 
 int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out, int32_t* pos) {

@@ -6,9 +6,10 @@
 
 namespace aur {
 
-// out[r] = w_tok[tok[r]] + w_pos[pos(r)], pos(r) = pos_dev ? pos_dev[r] : r % T.
+// out[r] = w_tok[tok[r]] + w_pos[pos(r)], pos(r) = pos_dev ? pos_dev[r] : r % T;
+// lens (optional): lens[r] = pos(r) + 1, the decode step's attention length.
 int embed_forward(aur_ctx* ctx, const float* w_tok, const float* w_pos, const uint32_t* tok,
-                  const int32_t* pos_dev, int T, float* out, int rows, int d);
+                  const int32_t* pos_dev, int T, float* out, int rows, int d, int32_t* lens = nullptr);
 // g_w_tok[tok_ids[u]] += Σ dy[row_idx[row_off[u]..row_off[u+1])]; g_w_pos[t] += Σ_b dy[b*T+t].
 int embed_backward(aur_ctx* ctx, const float* dy, int B, int T, int d, const uint32_t* tok_ids,
                    const int32_t* row_off, const int32_t* row_idx, int n_unique, float* g_w_tok,
@@ -40,7 +41,6 @@ int adamw(aur_ctx* ctx, float* p, const float* g, float* m1, float* m2, size_t n
 // K/V rows of a fused qkv [rows, 3d] into the history [B, max_len, d].
 int kv_store(aur_ctx* ctx, const float* qkv, int d, float* kh, float* vh, int max_len,
              const int32_t* pos_dev, int rows, int T);
-int lens_from_pos(aur_ctx* ctx, const int32_t* pos, int32_t* lens, int B);
 // out[r] = first argmax of logits row r; pos[r] += 1 when pos is non-null.
 int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out, int32_t* pos = nullptr);
 // dst[r] = src[(r*row_step + row_off) * ld_src .. + d]
