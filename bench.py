@@ -29,6 +29,10 @@ PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 PEAK_HBM = 8000.0       # GB/s
 
 COPY_MIB = 256          # calibration copy of the --only traffic leg
+# HBM bytes per head-GEMM launch from the two counter passes of
+# profiles/gemm_head_nt_8192x8192x512_traffic.md: FETCH_SIZE 133169.8 KiB × 2.000
+# + WRITE_SIZE 292192.8 KiB × 1.000 (factors from the 256 MiB copy).
+HEAD_TRAFFIC_BYTES = (133169.8 * 2.000 + 292192.8 * 1.000) * 1024
 SWEEP_KN = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
 M = 8192
 
@@ -353,7 +357,9 @@ def main() -> int:
         "decode": decode,
         "roofline": {"bound": "mfma", "kernel": "gemm_f32_mfma (tied head, NT 8192x8192x512)",
                      "achieved": round(head_tf, 3), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
-                     "frac": round(head_tf / PEAK_FP32_MFMA, 4), "traffic": None},
+                     "frac": round(head_tf / PEAK_FP32_MFMA, 4), "traffic": round(HEAD_TRAFFIC_BYTES),
+                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                     "algorithmic_bytes": 4 * (2 * 8192 * 512 + 8192 * 8192)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
