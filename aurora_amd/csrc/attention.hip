@@ -193,8 +193,11 @@ __global__ void __launch_bounds__(256) mha_fwd_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, l16 = lane & 15;
   const int nqt = (a.T + TQ - 1) / TQ;
-  const int qt = nqt - 1 - blockIdx.x;  // heaviest (longest) query tiles first
-  const int h = blockIdx.y, b = blockIdx.z;
+  // grid (H, B, tiles): the tile index varies slowest, so every (head,
+  // sequence)'s longest query tile is dispatched before any shorter one —
+  // longest-first over the whole launch, not just within a head.
+  const int qt = nqt - 1 - blockIdx.z;
+  const int h = blockIdx.x, b = blockIdx.y;
   const int q0 = qt * TQ;
   const size_t row_base = (size_t)b * a.T;
   const float* Qb = a.q + row_base * a.ld_qkv + h * DH;
@@ -322,8 +325,8 @@ __global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, l16 = lane & 15;
   const int nqt = (a.T + TQ - 1) / TQ;
-  const int qt = nqt - 1 - blockIdx.x;
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int qt = nqt - 1 - blockIdx.z;  // longest query tiles first (grid H, B, tiles)
+  const int h = blockIdx.x, b = blockIdx.y;
   const int q0 = qt * TQ;
   const size_t row_base = (size_t)b * a.T;
   const float* Qb = a.q + row_base * a.ld_qkv + h * DH;
@@ -388,8 +391,8 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, l16 = lane & 15;
   const int nqt = (a.T + TQ - 1) / TQ;
-  const int kt = blockIdx.x;  // key tile 0 has the most work: launched first
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int kt = blockIdx.z;  // key tile 0 has the most work: dispatched first (grid H, B, tiles)
+  const int h = blockIdx.x, b = blockIdx.y;
   const int k0 = kt * TQ;
   const size_t row_base = (size_t)b * a.T;
   const float* Qb = a.q + row_base * a.ld_qkv + h * DH;
@@ -526,13 +529,14 @@ int check_common(aur_ctx* ctx, uint32_t b, uint32_t t, uint32_t n_head, uint32_t
   if (b == 0 || t == 0 || n_head == 0) return aur::set_error(ctx, AUR_EINVAL, "attention: empty shape");
   if (ld_qkv < n_head * d_head || ld_o < n_head * d_head || (ld_qkv & 3) || (ld_o & 3))
     return aur::set_error(ctx, AUR_EINVAL, "attention: bad row stride (%u, %u)", ld_qkv, ld_o);
-  if (n_head > 65535 || b > 65535) return aur::set_error(ctx, AUR_ELIMIT, "attention: grid too large");
+  if (n_head > 65535 || b > 65535 || (t + TQ - 1) / TQ > 65535)
+    return aur::set_error(ctx, AUR_ELIMIT, "attention: grid too large");
   return 0;
 }
 
 template <int DH>
 void launch_fwd(const AttnArgs& a, int b, hipStream_t st) {
-  dim3 grid((a.T + TQ - 1) / TQ, a.H, b);
+  dim3 grid(a.H, b, (a.T + TQ - 1) / TQ);
   hipLaunchKernelGGL((mha_fwd_kernel<DH>), grid, dim3(256), 0, st, a);
 }
 
@@ -542,7 +546,7 @@ void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
   const size_t rows = (size_t)b * a.T * a.H;
   hipLaunchKernelGGL(mha_bwd_rowdot_kernel<DH>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256),
                      0, st, a, b);
-  dim3 grid((a.T + TQ - 1) / TQ, a.H, b);
+  dim3 grid(a.H, b, (a.T + TQ - 1) / TQ);
   hipLaunchKernelGGL((mha_bwd_dq_kernel<DH>), grid, dim3(256), 0, st, a);
   hipLaunchKernelGGL((mha_bwd_dkv_kernel<DH, 2>), grid, dim3(256), 0, st, a);
 }
