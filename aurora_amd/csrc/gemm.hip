@@ -264,6 +264,139 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
   }
 }
 
+// ------------------------------------------------ direct global→LDS path
+// Whole-tile shapes (M, N multiples of the tile, every K range a multiple of
+// 32, 16-byte aligned operands) load their tiles with global_load_lds_dwordx4:
+// the data goes from memory straight into LDS, with no register round trip
+// and no ds_write, so the waves spend their issue slots on fragment reads and
+// MFMAs (measured on MI355X at NT 8192×8192×512: 106 → 133 TFLOP/s).  A wave
+// load instruction fills 1 KB of consecutive LDS, so tiles are unpadded and
+// bank conflicts are avoided by an XOR swizzle of 16-byte granules:
+//   k-contiguous operand, [ROWS][32]: granule q of row r at q ^ ((r >> 1) & 7)
+//     (a b128 fragment read of rows r..r+15 at one k hits 16 distinct bank
+//     groups: row parity × the 8 swizzle values);
+//   k-strided operand, [32][ROWS]: granule q of k-row k at q ^ (((k >> 2) & 3) << 2)
+//     (the four k-rows 4g + s of a b32 fragment read land in 4 different
+//     granule groups).
+// The swizzle is an involution, so the same function maps physical → logical
+// on the load side.
+template <int ROWS, bool KCONTIG>
+struct DirectTile {
+  static constexpr int ELEMS = ROWS * 32;
+  static constexpr int GPR = KCONTIG ? 8 : ROWS / 4;       // 16-byte granules per LDS row
+  static constexpr int RPI = 64 / GPR;                     // LDS rows per wave instruction
+  static constexpr int NIW = (KCONTIG ? ROWS : 32) / RPI / 4;  // instructions per wave
+  static_assert(NIW >= 1, "tile too small for four waves");
+
+  __device__ static __forceinline__ int phys(int lrow, int q) {
+    return KCONTIG ? q ^ ((lrow >> 1) & 7) : q ^ (((lrow >> 2) & 3) << 2);
+  }
+  // This wave's share of the tile at (row origin r0, k origin k0).
+  __device__ static __forceinline__ void issue(const float* __restrict__ x, int ld, int r0, int k0,
+                                               float* lds, int w, int lane) {
+#pragma unroll
+    for (int j = 0; j < NIW; ++j) {
+      const int L0 = RPI * (NIW * w + j);
+      const int lrow = L0 + lane / GPR, q = phys(lrow, lane % GPR);
+      const float* src = KCONTIG ? x + (size_t)(r0 + lrow) * ld + k0 + 4 * q
+                                 : x + (size_t)(k0 + lrow) * ld + r0 + 4 * q;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds + L0 * GPR * 4), 16,
+                                       0, 0);
+    }
+  }
+  // f[s] = X(row, 16c + 4g + s), the same k permutation as read_frag.
+  __device__ static __forceinline__ floatx4 frag(const float* __restrict__ lds, int row, int c, int g) {
+    floatx4 f;
+    if (KCONTIG) {
+      f = *reinterpret_cast<const floatx4*>(lds + row * 32 + 4 * phys(row, 4 * c + g));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int k = 16 * c + 4 * g + e;
+        f[e] = lds[k * ROWS + 4 * phys(k, row >> 2) + (row & 3)];
+      }
+    }
+    return f;
+  }
+};
+
+template <int BM, int BN, bool AK, bool BKC>
+__global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
+  using TA = DirectTile<BM, AK>;
+  using TB = DirectTile<BN, BKC>;
+  constexpr int ST = TA::ELEMS + TB::ELEMS;
+  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
+  __shared__ __attribute__((aligned(1024))) float smem[2 * ST];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int g16 = lane >> 4, l16 = lane & 15;
+  // Tile order: as gemm_f32_mfma (contiguous run per XCD, 8-row groups).
+  constexpr int GM = 8;
+  const int ntiles = g.tiles_m * g.tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int per_group = GM * g.tiles_n;
+  const int first_m = (pid / per_group) * GM;
+  const int gsz = min(g.tiles_m - first_m, GM);
+  const int m0 = (first_m + (pid % per_group) % gsz) * BM, n0 = ((pid % per_group) / gsz) * BN;
+  const int kbeg = blockIdx.z * g.k_chunk;
+  const int nk = (min(g.K, kbeg + g.k_chunk) - kbeg) / 32;
+
+  floatx4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  if (nk > 0) {
+    TA::issue(g.A, g.lda, m0, kbeg, smem, wave, lane);
+    TB::issue(g.B, g.ldb, n0, kbeg, smem + TA::ELEMS, wave, lane);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const float* sa = smem + (kt & 1) * ST;
+    const float* sb = sa + TA::ELEMS;
+    if (kt + 1 < nk) {  // the other stage was released by the previous barrier
+      float* na = smem + ((kt + 1) & 1) * ST;
+      const int k0 = kbeg + (kt + 1) * 32;
+      TA::issue(g.A, g.lda, m0, k0, na, wave, lane);
+      TB::issue(g.B, g.ldb, n0, k0, na + TA::ELEMS, wave, lane);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      floatx4 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = TA::frag(sa, wm * WM + i * 16 + l16, c, g16);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = TB::frag(sb, wn * WN + j * 16 + l16, c, g16);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x4(fa[i][s], fb[j][s], acc[i][j]);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of the next stage landed
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * WN + j * 16 + l16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = m0 + wm * WM + i * 16 + 4 * g16 + e;
+        if (g.split)
+          g.P[((size_t)blockIdx.z * g.M + row) * g.N + col] = acc[i][j][e];
+        else
+          apply_epilogue(g.epi, g.C, (size_t)row * g.ldc + col, acc[i][j][e]);
+      }
+    }
+}
+
 // v(m,n) = Σ_{z=0..splits-1} P[z][m][n] summed in increasing z, then the
 // fused epilogue writes C (and C2).
 __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ P, float* __restrict__ C,
@@ -480,9 +613,9 @@ struct Plan {
 
 constexpr int kBK = 32;
 
-// Launch plan: tile shape and split-K count.  A CU holds two 128×128 or
-// 128×64 blocks (LDS) or four 64×64 ones, so a launch runs in "waves" of
-// CUs × occupancy blocks and a partly filled last wave idles the rest of
+// Launch plan: tile shape and split-K count.  A CU holds two 128×128, three
+// 128×64 or five 64×64 blocks (LDS of the direct-load kernel), so a launch
+// runs in "waves" of CUs × occupancy blocks and a partly filled last wave idles the rest of
 // the chip.  Each candidate (tile, splits) is scored by its wave
 // quantisation efficiency times the tile's measured relative MFMA
 // efficiency on MI355X (128×128: 1.00, 128×64: 0.90, 64×64: 0.88) times a
@@ -494,7 +627,7 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split) {
     int bm, bn, occ;
     double eff;
   };
-  static constexpr Cand cands[] = {{128, 128, 2, 1.00}, {128, 64, 2, 0.90}, {64, 64, 4, 0.88}};
+  static constexpr Cand cands[] = {{128, 128, 2, 1.00}, {128, 64, 3, 0.90}, {64, 64, 5, 0.88}};
   Plan p{128, 128, 1, K};
   double best = -1.0;
   for (const Cand& c : cands) {
@@ -534,7 +667,10 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split) {
 template <int BM, int BN, bool AK, bool BKC>
 void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st) {
   dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
-  if (vec)
+  const bool whole = vec && a.M % BM == 0 && a.N % BN == 0 && a.K % 32 == 0 && a.k_chunk % 32 == 0;
+  if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr)
+    hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC>), grid, dim3(kThreads), 0, st, a);
+  else if (vec)
     hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, kBK, AK, BKC, true>), grid, dim3(kThreads), 0, st, a);
   else
     hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, kBK, AK, BKC, false>), grid, dim3(kThreads), 0, st, a);
