@@ -72,6 +72,55 @@ __device__ __forceinline__ void apply_epilogue(const aur::Epilogue& e, float* __
   }
 }
 
+// Writes a wave's TM×TN grid of 16×16 accumulator tiles (lane holds rows
+// 4·g16 + e, column l16 of each) with the epilogue mode fixed at compile
+// time, so the store loops carry no per-element branch.  MODE −1: split-K
+// partial tile into P[z].  `full`: every row and column is in range.
+template <int MODE, int TM, int TN>
+__device__ __forceinline__ void write_tile(const GemmArgs& g, const floatx4 (&acc)[TM][TN], int r0, int c0,
+                                           int g16, int l16, bool full) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = c0 + j * 16 + l16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = r0 + i * 16 + 4 * g16 + e;
+        if (!full && (row >= g.M || col >= g.N)) continue;
+        const float v = acc[i][j][e];
+        if constexpr (MODE < 0) {
+          g.P[((size_t)blockIdx.z * g.M + row) * g.N + col] = v;
+        } else {
+          const size_t idx = (size_t)row * g.ldc + col;
+          if constexpr (MODE == aur::EPI_ACCUM) g.C[idx] = g.C[idx] + v;
+          else if constexpr (MODE == aur::EPI_RESID) g.C[idx] = g.epi.R[idx] + v;
+          else if constexpr (MODE == aur::EPI_GELU) {
+            g.C[idx] = v;
+            g.epi.C2[idx] = gelu_tanh(v);
+          } else if constexpr (MODE == aur::EPI_GELU_BWD) g.C[idx] = v * gelu_tanh_grad(g.epi.X[idx]);
+          else g.C[idx] = v;
+        }
+      }
+    }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void write_tiles(const GemmArgs& g, const floatx4 (&acc)[TM][TN], int r0, int c0,
+                                            int g16, int l16, bool full) {
+  if (g.split) {
+    write_tile<-1>(g, acc, r0, c0, g16, l16, full);
+    return;
+  }
+  switch (g.epi.mode) {
+    case aur::EPI_ACCUM: write_tile<aur::EPI_ACCUM>(g, acc, r0, c0, g16, l16, full); break;
+    case aur::EPI_RESID: write_tile<aur::EPI_RESID>(g, acc, r0, c0, g16, l16, full); break;
+    case aur::EPI_GELU: write_tile<aur::EPI_GELU>(g, acc, r0, c0, g16, l16, full); break;
+    case aur::EPI_GELU_BWD: write_tile<aur::EPI_GELU_BWD>(g, acc, r0, c0, g16, l16, full); break;
+    default: write_tile<aur::EPI_STORE>(g, acc, r0, c0, g16, l16, full); break;
+  }
+}
+
 template <int BM, int BN, int BK, bool AK, bool BKC>
 struct Smem {
   // k-contiguous operand: [rows][BK+4]; k-strided operand: [BK][cols+4].
@@ -244,24 +293,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
   }
 
   // Epilogue: lane holds D[4·g16 + e][l16] of each 16×16 tile.
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = n0 + wn * WN + j * 16 + l16;
-      if (col >= g.N) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = m0 + wm * WM + i * 16 + 4 * g16 + e;
-        if (row < g.M) {
-          if (g.split)
-            g.P[((size_t)blockIdx.z * g.M + row) * g.N + col] = acc[i][j][e];
-          else
-            apply_epilogue(g.epi, g.C, (size_t)row * g.ldc + col, acc[i][j][e]);
-        }
-      }
-    }
-  }
+  write_tiles(g, acc, m0 + wm * WM, n0 + wn * WN, g16, l16, m0 + BM <= g.M && n0 + BN <= g.N);
 }
 
 // ------------------------------------------------ direct global→LDS path
@@ -381,20 +413,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
     __syncthreads();
   }
 
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = n0 + wn * WN + j * 16 + l16;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = m0 + wm * WM + i * 16 + 4 * g16 + e;
-        if (g.split)
-          g.P[((size_t)blockIdx.z * g.M + row) * g.N + col] = acc[i][j][e];
-        else
-          apply_epilogue(g.epi, g.C, (size_t)row * g.ldc + col, acc[i][j][e]);
-      }
-    }
+  write_tiles(g, acc, m0 + wm * WM, n0 + wn * WN, g16, l16, /*full=*/true);
 }
 
 // v(m,n) = Σ_{z=0..splits-1} P[z][m][n] summed in increasing z, then the
