@@ -287,20 +287,37 @@ __global__ void __launch_bounds__(256) ln_param_partial_kernel(const float* __re
   pb[(size_t)chunk * d + c] = sb;
 }
 
-// dγ[c] += Σ_chunk pg[chunk][c], dβ[c] += Σ_chunk pb[chunk][c] (chunk ascending).
+// dγ[c] += Σ_chunk pg[chunk][c], dβ[c] += Σ_chunk pb[chunk][c].  A block owns
+// 16 columns; its 256 threads are 16 columns × 16 chunk classes (chunk ≡ q
+// mod 16, summed ascending), and the 16 class sums are added in class order
+// through LDS — a fixed order, so the result is deterministic, with 16× the
+// parallelism of one thread per column.
 __global__ void __launch_bounds__(256) ln_param_final_kernel(const float* __restrict__ pg,
                                                              const float* __restrict__ pb,
                                                              int nchunks, float* __restrict__ dgamma,
                                                              float* __restrict__ dbeta, int d) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= d) return;
+  __shared__ float sg_[16][17], sb_[16][17];
+  const int col = threadIdx.x & 15, q = threadIdx.x >> 4;
+  const int c = blockIdx.x * 16 + col;
   float sg = 0.f, sb = 0.f;
-  for (int k = 0; k < nchunks; ++k) {
-    sg += pg[(size_t)k * d + c];
-    sb += pb[(size_t)k * d + c];
+  if (c < d)
+    for (int k = q; k < nchunks; k += 16) {
+      sg += pg[(size_t)k * d + c];
+      sb += pb[(size_t)k * d + c];
+    }
+  sg_[q][col] = sg;
+  sb_[q][col] = sb;
+  __syncthreads();
+  if (q == 0 && c < d) {
+    float tg = 0.f, tb = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      tg += sg_[i][col];
+      tb += sb_[i][col];
+    }
+    dgamma[c] += tg;
+    dbeta[c] += tb;
   }
-  dgamma[c] += sg;
-  dbeta[c] += sb;
 }
 
 // ---------------------------------------------------------------- softmax-CE
@@ -530,7 +547,7 @@ int layer_norm_backward(aur_ctx* ctx, const float* x, const float* mean, const f
   float* pb = ws + (size_t)nch * d;
   hipLaunchKernelGGL(ln_param_partial_kernel, dim3((d + 255) / 256, nch), dim3(256), 0, ctx->stream, x,
                      mean, rstd, dy, pg, pb, rows, d);
-  hipLaunchKernelGGL(ln_param_final_kernel, dim3((d + 255) / 256), dim3(256), 0, ctx->stream, pg, pb, nch,
+  hipLaunchKernelGGL(ln_param_final_kernel, dim3((d + 15) / 16), dim3(256), 0, ctx->stream, pg, pb, nch,
                      dgamma, dbeta, d);
   LAUNCH_OK(ctx, "ln_bwd kernels");
 }
