@@ -55,6 +55,11 @@ SIGNATURES: dict[str, tuple] = {
     "aur_model_tensor": (_i32, [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32,
                                 C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
     "aur_model_zero_grad": (_i32, [C.c_void_p]),
+    "aur_checkpoint_peek": (_i32, [C.c_char_p, C.c_void_p, C.POINTER(_u32), C.POINTER(_u32),
+                                   C.POINTER(C.c_uint64)]),
+    "aur_model_load_checkpoint": (_i32, [C.c_void_p, C.c_char_p, C.POINTER(_u32),
+                                         C.POINTER(C.c_uint64)]),
+    "aur_model_save_checkpoint": (_i32, [C.c_void_p, C.c_char_p, _u32, C.c_uint64]),
     "aur_model_train_step_batch": (_i32, [C.c_void_p, C.c_void_p, C.c_void_p, _u32, _u32,
                                           C.POINTER(C.c_float)]),
     "aur_model_forward": (_i32, [C.c_void_p, C.c_void_p, _u32, _u32, C.c_void_p]),

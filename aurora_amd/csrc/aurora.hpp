@@ -20,6 +20,7 @@
 #pragma once
 
 #include <cstdint>
+#include <cstdio>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -174,6 +175,18 @@ struct AdamWConfig {
 
 class KvCacheGpu;
 
+// Header of an AURORA05/06/07 checkpoint (src/checkpoint.rs:9-49).
+struct CheckpointHeader {
+  int version = 0;  // 5, 6 or 7
+  TransformerConfig cfg;
+  uint32_t flags = 0;  // rope, rmsnorm, relu2, qk_norm, untied_head, swiglu, layerscale, parallel, diff_attn, head_bias
+  float softcap = 0.f;
+  uint32_t canon_kernel = 0, sink_tokens = 0, epoch = 0;
+  uint64_t step = 0;
+};
+CheckpointHeader read_checkpoint_header(const char* path);
+CheckpointHeader read_checkpoint_header(std::FILE* f);
+
 // The reference's DecoderTransformerGpu at M = B·T rows: B sequences of
 // length T run through every GEMM together (the reference serialises them,
 // one sequence per GEMM).  Gradient convention: per-sequence mean-over-T
@@ -209,6 +222,14 @@ class DecoderTransformerGpu {
   void step_adamw(const AdamWConfig& cfg);
   // clip_grads + step_adamw without the separate scaling pass.
   float clip_and_step_adamw(float max_norm, const AdamWConfig& cfg);
+
+  // Zero the optimizer state (AdamW moments) — a fresh optimizer.
+  void reset_optimizer_state();
+  // checkpoint.rs save / load (AURORA07 writes; AURORA05-07 reads).  load
+  // requires this model's dimensions, refuses optional features the
+  // backend lacks (AUR_ELIMIT), resets the optimizer state and sets `step`.
+  void save_checkpoint(const char* path, uint32_t epoch, uint64_t step) const;
+  CheckpointHeader load_checkpoint(const char* path);
 
   // KV decode (src/gpu/transformer.rs:2374-2640, batched).
   void prefill_kv(KvCacheGpu& cache, const uint32_t* tokens, uint32_t b, uint32_t t, float* last_logits);

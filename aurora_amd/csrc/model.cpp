@@ -409,6 +409,10 @@ inline float powi_f(float b, uint64_t e) {
 }
 }  // namespace
 
+void DecoderTransformerGpu::reset_optimizer_state() {
+  ck(ctx_, aur_memset0(ctx_, m1_, 2 * n_params_ * sizeof(float)), "zero moments");
+}
+
 void DecoderTransformerGpu::step_adamw(const AdamWConfig& c) {
   step += 1;
   const float bc1 = 1.0f - powi_f(c.beta1, step), bc2 = 1.0f - powi_f(c.beta2, step);
@@ -640,12 +644,10 @@ int guard(aur_ctx* ctx, F&& f) {
   try {
     f();
     return 0;
-  } catch (const aurora::Error& e) {
-    if (ctx) ctx->last_error = e.what();
-    return e.code ? e.code : AUR_EINVAL;
+  } catch (const aurora::Error& e) {  // ctx == nullptr: the library-wide slot of aur_last_error(NULL)
+    return aur::set_error(ctx, e.code ? e.code : AUR_EINVAL, "%s", e.what());
   } catch (const std::exception& e) {
-    if (ctx) ctx->last_error = e.what();
-    return AUR_EINVAL;
+    return aur::set_error(ctx, AUR_EINVAL, "%s", e.what());
   }
 }
 }  // namespace
@@ -681,6 +683,32 @@ int aur_model_tensor(aur_model* m, const char* name, int32_t layer, int32_t grad
 int aur_model_zero_grad(aur_model* m) {
   if (!m) return AUR_EINVAL;
   return guard(m->m->ctx(), [&] { m->m->zero_grad(); });
+}
+
+int aur_checkpoint_peek(const char* path, aur_model_config* cfg, uint32_t* flags, uint32_t* epoch,
+                        uint64_t* step) {
+  return guard(nullptr, [&] {
+    const aurora::CheckpointHeader h = aurora::read_checkpoint_header(path);
+    if (cfg) *cfg = aur_model_config{h.cfg.vocab, h.cfg.d_model, h.cfg.n_layer, h.cfg.n_head, h.cfg.d_ff,
+                                     h.cfg.seq_len_max};
+    if (flags) *flags = h.flags;
+    if (epoch) *epoch = h.epoch;
+    if (step) *step = h.step;
+  });
+}
+
+int aur_model_load_checkpoint(aur_model* m, const char* path, uint32_t* epoch, uint64_t* step) {
+  if (!m) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] {
+    const aurora::CheckpointHeader h = m->m->load_checkpoint(path);
+    if (epoch) *epoch = h.epoch;
+    if (step) *step = h.step;
+  });
+}
+
+int aur_model_save_checkpoint(aur_model* m, const char* path, uint32_t epoch, uint64_t step) {
+  if (!m) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] { m->m->save_checkpoint(path, epoch, step); });
 }
 
 int aur_model_train_step_batch(aur_model* m, const uint32_t* tokens, const uint32_t* targets, uint32_t b,

@@ -21,6 +21,17 @@ class ModelConfig(C.Structure):
                 ("n_head", C.c_uint32), ("d_ff", C.c_uint32), ("seq_len_max", C.c_uint32)]
 
 
+def peek_checkpoint(path):
+    """Header of an AURORA05/06/07 file: (ModelConfig, flags, epoch, step)."""
+    lib = _lib.load()
+    cfg, flags, epoch, step = ModelConfig(), C.c_uint32(), C.c_uint32(), C.c_uint64()
+    rc = lib.aur_checkpoint_peek(str(path).encode(), C.byref(cfg), C.byref(flags), C.byref(epoch),
+                                 C.byref(step))
+    if rc != 0:
+        raise _lib.AuroraError("aur_checkpoint_peek", rc, lib.aur_last_error(None).decode())
+    return cfg, flags.value, epoch.value, step.value
+
+
 def _u32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.uint32)
 
@@ -76,6 +87,27 @@ class DecoderTransformerGpu:
 
     def zero_grad(self) -> None:
         self._call("aur_model_zero_grad")
+
+    # ---- AURORA07 checkpoints (src/checkpoint.rs) ----
+    def save_checkpoint(self, path, epoch: int = 0, step: int = 0) -> None:
+        """checkpoint::save: AURORA07, every optional feature off."""
+        self._call("aur_model_save_checkpoint", str(path).encode(), epoch, step)
+
+    def load_checkpoint(self, path) -> tuple[int, int]:
+        """checkpoint::load into this model (same dimensions): parameters,
+        fresh optimizer moments, optimizer step = the stored step.
+        Returns (epoch, step)."""
+        e, st = C.c_uint32(), C.c_uint64()
+        self._call("aur_model_load_checkpoint", str(path).encode(), C.byref(e), C.byref(st))
+        return e.value, st.value
+
+    @classmethod
+    def from_checkpoint(cls, ctx: GpuContext, path, max_batch: int):
+        """A model sized from the checkpoint's header, then loaded from it."""
+        cfg, flags, epoch, step = peek_checkpoint(path)
+        m = cls(ctx, cfg.vocab, cfg.d_model, cfg.n_layer, cfg.n_head, cfg.d_ff, cfg.seq_len_max, max_batch)
+        m.load_checkpoint(path)
+        return m
 
     def train_step_batch(self, tokens, targets) -> float:
         tok, tgt = _u32(tokens), _u32(targets)

@@ -36,6 +36,7 @@ typedef struct aur_ctx aur_ctx;
 #define AUR_EINVAL 10001   /* bad argument (shape, null pointer, alignment) */
 #define AUR_ENOMEM 10002   /* workspace could not be obtained */
 #define AUR_ELIMIT 10003   /* shape exceeds a documented kernel limit */
+#define AUR_EIO 10004      /* checkpoint file could not be opened, read or written */
 
 /* ---- context / runtime (replaces src/gpu/context.rs:22-69 GpuContext::new
  *      and src/gpu/buffers.rs:27-191 GpuBuffer) ------------------------- */
@@ -199,6 +200,22 @@ int aur_model_tensor(aur_model* m, const char* name, int32_t layer, int32_t grad
                      size_t* len);
 /* zero_grad (transformer.rs:1242). */
 int aur_model_zero_grad(aur_model* m);
+
+/* ---- AURORA07 checkpoints (src/checkpoint.rs) ------------------------------
+ * aur_checkpoint_peek reads the header of an AURORA05/06/07 file: the model
+ * dimensions, the feature flags word (checkpoint.rs:70-79), epoch and step.
+ * aur_model_load_checkpoint (checkpoint.rs:188-301 `load`, into an existing
+ * model of the same dimensions): fills every parameter, zeroes the optimizer
+ * moments and sets the optimizer step to the stored one; AUR_ELIMIT when the
+ * file uses an optional feature this backend does not implement (any flag,
+ * softcap, canon kernel, sink tokens), AUR_EINVAL on a bad magic or other
+ * dimensions, AUR_EIO when the file cannot be read or ends early.
+ * aur_model_save_checkpoint (checkpoint.rs:84-186 `save`): writes AURORA07
+ * with every optional feature off. */
+int aur_checkpoint_peek(const char* path, aur_model_config* cfg, uint32_t* flags, uint32_t* epoch,
+                        uint64_t* step);
+int aur_model_load_checkpoint(aur_model* m, const char* path, uint32_t* epoch, uint64_t* step);
+int aur_model_save_checkpoint(aur_model* m, const char* path, uint32_t epoch, uint64_t step);
 /* train_step_batch (transformer.rs:1571): forward + softmax-CE + backward for
  * b host sequences of length t (tokens/targets [b*t]); gradients accumulate
  * as the batch MEAN of per-sequence mean-over-t losses (the CPU trainer's
