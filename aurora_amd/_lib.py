@@ -55,6 +55,10 @@ SIGNATURES: dict[str, tuple] = {
     "aur_model_tensor": (_i32, [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32,
                                 C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
     "aur_model_zero_grad": (_i32, [C.c_void_p]),
+    "aur_model_step_muon_hybrid": (_i32, [C.c_void_p, C.c_float, C.c_float, C.c_int32, C.c_float,
+                                          _u32, C.c_float, C.c_float, C.c_float, C.c_float,
+                                          C.c_float]),
+    "aur_model_clip_grads_adamw_subset": (_i32, [C.c_void_p, C.c_float, C.POINTER(C.c_float)]),
     "aur_checkpoint_peek": (_i32, [C.c_char_p, C.c_void_p, C.POINTER(_u32), C.POINTER(_u32),
                                    C.POINTER(C.c_uint64)]),
     "aur_model_load_checkpoint": (_i32, [C.c_void_p, C.c_char_p, C.POINTER(_u32),

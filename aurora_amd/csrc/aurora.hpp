@@ -173,6 +173,14 @@ struct AdamWConfig {
   float lr = 6e-4f, beta1 = 0.9f, beta2 = 0.95f, eps = 1e-8f, weight_decay = 0.1f;
 };
 
+// src/optimizer.rs:94-113
+struct MuonConfig {
+  float lr = 0.02f, momentum = 0.95f;
+  bool nesterov = true;
+  float weight_decay = 0.0f;
+  uint32_t ns_steps = 5;
+};
+
 class KvCacheGpu;
 
 // Header of an AURORA05/06/07 checkpoint (src/checkpoint.rs:9-49).
@@ -223,7 +231,17 @@ class DecoderTransformerGpu {
   // clip_grads + step_adamw without the separate scaling pass.
   float clip_and_step_adamw(float max_norm, const AdamWConfig& cfg);
 
-  // Zero the optimizer state (AdamW moments) — a fresh optimizer.
+  // Muon hybrid (model.rs:1023-1090, gpu/transformer.rs:2052-2291): AdamW on
+  // the embeddings and LayerNorm γ/β, Muon (momentum → Frobenius bound →
+  // ns_steps quintic Newton–Schulz on the GEMMs → √(max/min) scale) on every
+  // Q/K/V/O/fc/proj matrix.  The Muon momentum buffers are allocated on the
+  // first call.
+  void step_muon_hybrid(const MuonConfig& muon, const AdamWConfig& adam);
+  // model.rs:1101-1107: L2 norm over the AdamW subset only, which is scaled
+  // to max_norm when above it; returns the pre-clip norm.
+  float clip_grads_adamw_subset(float max_norm);
+
+  // Zero the optimizer state (AdamW moments, Muon momentum) — a fresh optimizer.
   void reset_optimizer_state();
   // checkpoint.rs save / load (AURORA07 writes; AURORA05-07 reads).  load
   // requires this model's dimensions, refuses optional features the
@@ -250,6 +268,10 @@ class DecoderTransformerGpu {
   uint32_t max_batch_;
   size_t n_params_ = 0, n_decay_ = 0;
   void* state_mem_ = nullptr;  // params | grads | m1 | m2
+  void* muon_mem_ = nullptr;   // Muon momentum of the matrix region + Newton–Schulz scratch
+  float *mu_ = nullptr, *ns_upd_ = nullptr, *ns_x_[2] = {nullptr, nullptr}, *ns_bx_ = nullptr;
+  float *ns_a_ = nullptr, *ns_a2_ = nullptr, *ns_b_ = nullptr, *muon_stats_ = nullptr;
+  void muon_matrix(float* p, const float* g, float* mu, uint32_t rows, uint32_t cols, const MuonConfig& c);
   void* act_mem_ = nullptr;
   float *params_ = nullptr, *grads_ = nullptr, *m1_ = nullptr, *m2_ = nullptr;
   std::vector<Layer>* layers_ = nullptr;

@@ -198,6 +198,7 @@ DecoderTransformerGpu::~DecoderTransformerGpu() {
     aur_sync(ctx_);
     aur_free(ctx_, act_mem_);
     aur_free(ctx_, state_mem_);
+    if (muon_mem_) aur_free(ctx_, muon_mem_);
   }
   delete layers_;
   delete acts_;
@@ -411,6 +412,112 @@ inline float powi_f(float b, uint64_t e) {
 
 void DecoderTransformerGpu::reset_optimizer_state() {
   ck(ctx_, aur_memset0(ctx_, m1_, 2 * n_params_ * sizeof(float)), "zero moments");
+  if (mu_) ck(ctx_, aur_memset0(ctx_, mu_, (n_decay_ - (size_t)cfg_.vocab * cfg_.d_model) * sizeof(float)),
+              "zero muon momentum");
+}
+
+// ------------------------------------------------------------------ Muon
+// The matrix parameters (per layer w_q, w_k, w_v = the rows of w_qkv, w_o,
+// w_fc, w_proj) occupy [V·d, n_decay) of the flat buffers; the Muon momentum
+// buffer mirrors that region.  Newton–Schulz scratch is sized for the
+// largest matrix: m = min(rows, cols) = d for every one, n = max ≤ d_ff.
+float DecoderTransformerGpu::clip_grads_adamw_subset(float max_norm) {
+  auto& A = *acts_;
+  const size_t n_tok = (size_t)cfg_.vocab * cfg_.d_model, n_rest = n_params_ - n_decay_;
+  ck(ctx_, aur::grad_norm2(ctx_, grads_, n_tok, grads_ + n_decay_, n_rest, max_norm, A.norm_part, A.stats),
+     "subset norm");
+  ck(ctx_, aur::scale_by(ctx_, grads_, n_tok, A.stats + 1), "subset clip");
+  ck(ctx_, aur::scale_by(ctx_, grads_ + n_decay_, n_rest, A.stats + 1), "subset clip");
+  float nrm = 0.f;
+  ck(ctx_, aur_d2h(ctx_, &nrm, A.stats, 4), "download norm");
+  return nrm;
+}
+
+void DecoderTransformerGpu::muon_matrix(float* p, const float* g, float* mu, uint32_t rows, uint32_t cols,
+                                        const MuonConfig& c) {
+  const size_t n = (size_t)rows * cols;
+  const int m = (int)std::min(rows, cols), nn = (int)std::max(rows, cols);
+  const bool transposed = rows > cols;
+  auto& A = *acts_;
+  aur::Epilogue store;
+  ck(ctx_, aur::muon_momentum(ctx_, g, mu, ns_upd_, n, c.momentum, c.nesterov), "muon momentum");
+  ck(ctx_, aur::frob_inv(ctx_, ns_upd_, n, A.norm_part, muon_stats_), "muon frobenius");
+  ck(ctx_, aur::scale_by(ctx_, ns_upd_, n, muon_stats_ + 1), "muon frobenius scale");
+  // X: the update in wide orientation [m × nn] (optimizer.rs:180-191).
+  float* x = ns_upd_;
+  int cur = 0;
+  if (transposed) {
+    ck(ctx_, aur::transpose(ctx_, ns_upd_, ns_x_[0], (int)rows, (int)cols), "muon load");
+    x = ns_x_[0];
+    cur = 0;
+  }
+  const float a_coef = 3.4445f, b_coef = -4.7750f, c_coef = 2.0315f;
+  for (uint32_t it = 0; it < c.ns_steps; ++it) {
+    float* nxt = (x == ns_x_[0]) ? ns_x_[1] : ns_x_[0];
+    // A = X·Xᵀ, A² = A·A, B = b·A + c·A², X' = a·X + B·X  (optimizer.rs:197-239)
+    ck(ctx_, aur::gemm(ctx_, true, true, x, nn, x, nn, ns_a_, m, m, m, nn, store), "ns xxt");
+    ck(ctx_, aur::gemm(ctx_, true, false, ns_a_, m, ns_a_, m, ns_a2_, m, m, m, m, store), "ns aa");
+    ck(ctx_, aur::axpby(ctx_, ns_b_, b_coef, ns_a_, c_coef, ns_a2_, (size_t)m * m), "ns combine");
+    ck(ctx_, aur::gemm(ctx_, true, false, ns_b_, m, x, nn, ns_bx_, nn, m, nn, m, store), "ns bx");
+    ck(ctx_, aur::axpby(ctx_, nxt, a_coef, x, 1.0f, ns_bx_, (size_t)m * nn), "ns step");
+    x = nxt;
+  }
+  (void)cur;
+  const float* upd = x;
+  if (transposed) {
+    ck(ctx_, aur::transpose(ctx_, x, ns_upd_, m, nn), "muon store");
+    upd = ns_upd_;
+  }
+  const float scale = std::sqrt((float)nn / (float)m);
+  ck(ctx_, aur::muon_apply(ctx_, p, upd, n, c.lr * scale, c.lr * c.weight_decay), "muon apply");
+}
+
+void DecoderTransformerGpu::step_muon_hybrid(const MuonConfig& mc, const AdamWConfig& ac) {
+  const size_t d = cfg_.d_model, F = cfg_.d_ff, n_tok = (size_t)cfg_.vocab * d;
+  if (!muon_mem_) {
+    const size_t n_mat = n_decay_ - n_tok;
+    const size_t big = d * std::max(d, F), sq = d * d;
+    const size_t floats = n_mat + 4 * big + 3 * sq + 64;
+    ck(ctx_, aur_malloc(ctx_, floats * sizeof(float) + 8 * 256, &muon_mem_), "alloc muon state");
+    Carver cv{static_cast<char*>(muon_mem_)};
+    mu_ = cv.take<float>(n_mat);
+    ns_upd_ = cv.take<float>(big);
+    ns_x_[0] = cv.take<float>(big);
+    ns_x_[1] = cv.take<float>(big);
+    ns_bx_ = cv.take<float>(big);
+    ns_a_ = cv.take<float>(sq);
+    ns_a2_ = cv.take<float>(sq);
+    ns_b_ = cv.take<float>(sq);
+    muon_stats_ = cv.take<float>(64);
+    ck(ctx_, aur_memset0(ctx_, mu_, n_mat * sizeof(float)), "zero muon momentum");
+  }
+  // model.rs:1031-1032: one shared step counter for the AdamW bias correction.
+  step += 1;
+  const float bc1 = 1.0f - powi_f(ac.beta1, step), bc2 = 1.0f - powi_f(ac.beta2, step);
+  // AdamW subset (model.rs:1039-1078): w_tok with decay (embed_lr_mult = 1,
+  // the reference default), then w_pos and every LayerNorm γ/β without.
+  ck(ctx_, aur::adamw(ctx_, params_, grads_, m1_, m2_, n_tok, n_tok, nullptr, ac.lr, ac.beta1, ac.beta2,
+                      ac.eps, ac.weight_decay, bc1, bc2),
+     "adamw w_tok");
+  ck(ctx_, aur::adamw(ctx_, params_ + n_decay_, grads_ + n_decay_, m1_ + n_decay_, m2_ + n_decay_,
+                      n_params_ - n_decay_, 0, nullptr, ac.lr, ac.beta1, ac.beta2, ac.eps, ac.weight_decay,
+                      bc1, bc2),
+     "adamw undecayed");
+  // Muon matrices, in the reference's order (gpu/transformer.rs:836-866):
+  // rows × cols as it passes them (w_fc as d × d_ff, w_proj as d_ff × d).
+  for (uint32_t l = 0; l < cfg_.n_layer; ++l) {
+    Layer& Y = (*layers_)[l];
+    auto go = [&](float* p, uint32_t rows, uint32_t cols) {
+      const size_t off = (size_t)(p - params_);
+      muon_matrix(p, grads_ + off, mu_ + (off - n_tok), rows, cols, mc);
+    };
+    go(Y.w_qkv, (uint32_t)d, (uint32_t)d);
+    go(Y.w_qkv + d * d, (uint32_t)d, (uint32_t)d);
+    go(Y.w_qkv + 2 * d * d, (uint32_t)d, (uint32_t)d);
+    go(Y.w_o, (uint32_t)d, (uint32_t)d);
+    go(Y.w_fc, (uint32_t)d, (uint32_t)F);
+    go(Y.w_proj, (uint32_t)F, (uint32_t)d);
+  }
 }
 
 void DecoderTransformerGpu::step_adamw(const AdamWConfig& c) {
@@ -683,6 +790,35 @@ int aur_model_tensor(aur_model* m, const char* name, int32_t layer, int32_t grad
 int aur_model_zero_grad(aur_model* m) {
   if (!m) return AUR_EINVAL;
   return guard(m->m->ctx(), [&] { m->m->zero_grad(); });
+}
+
+int aur_model_step_muon_hybrid(aur_model* m, float muon_lr, float momentum, int32_t nesterov, float muon_wd,
+                               uint32_t ns_steps, float lr, float beta1, float beta2, float eps,
+                               float weight_decay) {
+  if (!m) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] {
+    aurora::MuonConfig mc;
+    mc.lr = muon_lr;
+    mc.momentum = momentum;
+    mc.nesterov = nesterov != 0;
+    mc.weight_decay = muon_wd;
+    mc.ns_steps = ns_steps;
+    aurora::AdamWConfig ac;
+    ac.lr = lr;
+    ac.beta1 = beta1;
+    ac.beta2 = beta2;
+    ac.eps = eps;
+    ac.weight_decay = weight_decay;
+    m->m->step_muon_hybrid(mc, ac);
+  });
+}
+
+int aur_model_clip_grads_adamw_subset(aur_model* m, float max_norm, float* norm) {
+  if (!m) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] {
+    const float n = m->m->clip_grads_adamw_subset(max_norm);
+    if (norm) *norm = n;
+  });
 }
 
 int aur_checkpoint_peek(const char* path, aur_model_config* cfg, uint32_t* flags, uint32_t* epoch,

@@ -365,9 +365,12 @@ __global__ void __launch_bounds__(256) sumsq_partial_kernel(const float* __restr
   if (threadIdx.x == 0) part[blockIdx.x] = s;
 }
 
-// stats[0] = ‖g‖₂, stats[1] = clip factor (max_norm/‖g‖ if ‖g‖ > max_norm > 0, else 1).
+// stats[0] = ‖g‖₂ and stats[1] = the clip factor (max_norm/‖g‖ if
+// ‖g‖ > max_norm > 0, else 1) — or, with frob_inv, 1/(‖g‖ + 1e-7): Muon's
+// Frobenius bound before Newton–Schulz (src/gpu/muon.rs:112-156).
 __global__ void __launch_bounds__(256) norm_final_kernel(const float* __restrict__ part, int nparts,
-                                                         float max_norm, float* __restrict__ stats) {
+                                                         float max_norm, float* __restrict__ stats,
+                                                         int frob_inv) {
   __shared__ float red[4];
   float s = 0.f;
   for (int i = threadIdx.x; i < nparts; i += 256) s += part[i];
@@ -375,7 +378,10 @@ __global__ void __launch_bounds__(256) norm_final_kernel(const float* __restrict
   if (threadIdx.x == 0) {
     const float nrm = sqrtf(s);
     stats[0] = nrm;
-    stats[1] = (max_norm > 0.f && nrm > max_norm && nrm > 0.f) ? max_norm / nrm : 1.0f;
+    if (frob_inv)
+      stats[1] = 1.0f / (nrm + 1e-7f);
+    else
+      stats[1] = (max_norm > 0.f && nrm > max_norm && nrm > 0.f) ? max_norm / nrm : 1.0f;
   }
 }
 
@@ -410,6 +416,61 @@ __global__ void __launch_bounds__(256) scale_kernel(float* __restrict__ x, size_
   if (cf == 1.0f) return;
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] *= cf;
+}
+
+// ---------------------------------------------------------------- Muon
+// m = β·m + g; update = nesterov ? g + β·m : m   (src/optimizer.rs:273-285,
+// src/gpu/muon.rs:18-37).
+__global__ void __launch_bounds__(256) muon_momentum_kernel(const float* __restrict__ g, float* __restrict__ m,
+                                                            float* __restrict__ upd, size_t n, float beta,
+                                                            int nesterov) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float gi = g[i];
+    const float mn = beta * m[i] + gi;
+    m[i] = mn;
+    upd[i] = nesterov ? gi + beta * mn : mn;
+  }
+}
+
+// out = α·x + β·y — the Newton–Schulz combines B = b·A + c·A² and
+// X' = a·X + B·X (src/gpu/muon.rs:421-515).
+__global__ void __launch_bounds__(256) axpby_kernel(float* __restrict__ out, float alpha,
+                                                    const float* __restrict__ x, float beta,
+                                                    const float* __restrict__ y, size_t n) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = alpha * x[i] + beta * y[i];
+}
+
+// dst[c][r] = src[r][c] for src [rows × cols], through 32×33 LDS tiles so
+// both sides are coalesced (src/gpu/muon.rs:204-271 load/store).
+__global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                        int rows, int cols) {
+  __shared__ float t[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 8 rows per pass
+  for (int i = ty; i < 32; i += 8) {
+    const int r = r0 + i, c = c0 + tx;
+    if (r < rows && c < cols) t[i][tx] = src[(size_t)r * cols + c];
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int c = c0 + i, r = r0 + tx;
+    if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][i];
+  }
+}
+
+// params -= lr·scale·update + lr·wd·params   (src/optimizer.rs:292-304,
+// src/gpu/muon.rs:517-560; decoupled decay applies to every Muon matrix).
+__global__ void __launch_bounds__(256) muon_apply_kernel(float* __restrict__ p, const float* __restrict__ upd,
+                                                         size_t n, float lr_scale, float lr_wd) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float step = lr_scale * upd[i];
+    if (lr_wd != 0.f) step += lr_wd * p[i];
+    p[i] -= step;
+  }
 }
 
 // ------------------------------------------------------------------ KV cache
@@ -564,11 +625,51 @@ constexpr int kNormParts = 1024;
 int grad_norm(aur_ctx* ctx, const float* g, size_t n, float max_norm, float* part, float* stats) {
   hipLaunchKernelGGL(sumsq_partial_kernel, dim3(kNormParts), dim3(256), 0, ctx->stream, g, n, part);
   hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(256), 0, ctx->stream, part, kNormParts, max_norm,
-                     stats);
+                     stats, 0);
   LAUNCH_OK(ctx, "grad norm kernels");
 }
 
+int grad_norm2(aur_ctx* ctx, const float* g1, size_t n1, const float* g2, size_t n2, float max_norm,
+               float* part, float* stats) {
+  hipLaunchKernelGGL(sumsq_partial_kernel, dim3(kNormParts / 2), dim3(256), 0, ctx->stream, g1, n1, part);
+  hipLaunchKernelGGL(sumsq_partial_kernel, dim3(kNormParts / 2), dim3(256), 0, ctx->stream, g2, n2,
+                     part + kNormParts / 2);
+  hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(256), 0, ctx->stream, part, kNormParts, max_norm,
+                     stats, 0);
+  LAUNCH_OK(ctx, "grad norm kernels");
+}
+
+int frob_inv(aur_ctx* ctx, const float* x, size_t n, float* part, float* stats) {
+  hipLaunchKernelGGL(sumsq_partial_kernel, dim3(kNormParts), dim3(256), 0, ctx->stream, x, n, part);
+  hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(256), 0, ctx->stream, part, kNormParts, 0.f, stats,
+                     1);
+  LAUNCH_OK(ctx, "frobenius kernels");
+}
+
 size_t grad_norm_ws_floats() { return kNormParts; }
+
+int muon_momentum(aur_ctx* ctx, const float* g, float* m, float* upd, size_t n, float beta, bool nesterov) {
+  hipLaunchKernelGGL(muon_momentum_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, g, m, upd, n, beta,
+                     nesterov ? 1 : 0);
+  LAUNCH_OK(ctx, "muon_momentum_kernel");
+}
+
+int axpby(aur_ctx* ctx, float* out, float alpha, const float* x, float beta, const float* y, size_t n) {
+  hipLaunchKernelGGL(axpby_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, out, alpha, x, beta, y, n);
+  LAUNCH_OK(ctx, "axpby_kernel");
+}
+
+int transpose(aur_ctx* ctx, const float* src, float* dst, int rows, int cols) {
+  hipLaunchKernelGGL(transpose_kernel, dim3((cols + 31) / 32, (rows + 31) / 32), dim3(256), 0, ctx->stream,
+                     src, dst, rows, cols);
+  LAUNCH_OK(ctx, "transpose_kernel");
+}
+
+int muon_apply(aur_ctx* ctx, float* p, const float* upd, size_t n, float lr_scale, float lr_wd) {
+  hipLaunchKernelGGL(muon_apply_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, p, upd, n, lr_scale,
+                     lr_wd);
+  LAUNCH_OK(ctx, "muon_apply_kernel");
+}
 
 int scale_by(aur_ctx* ctx, float* x, size_t n, const float* factor) {
   hipLaunchKernelGGL(scale_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, x, n, factor);

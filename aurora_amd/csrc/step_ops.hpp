@@ -34,6 +34,17 @@ int softmax_ce(aur_ctx* ctx, float* logits, const uint32_t* targets, float* nll,
 // stats[0] = ‖g‖₂ over n floats, stats[1] = clip factor for max_norm.
 int grad_norm(aur_ctx* ctx, const float* g, size_t n, float max_norm, float* part, float* stats);
 size_t grad_norm_ws_floats();
+// The same over two ranges (g1[0, n1) and g2[0, n2)): the AdamW subset of a
+// Muon step (embeddings + LayerNorm, model.rs:514-560).
+int grad_norm2(aur_ctx* ctx, const float* g1, size_t n1, const float* g2, size_t n2, float max_norm,
+               float* part, float* stats);
+// stats[0] = ‖x‖_F, stats[1] = 1/(‖x‖_F + 1e-7).
+int frob_inv(aur_ctx* ctx, const float* x, size_t n, float* part, float* stats);
+// Muon pieces (optimizer.rs:147-305, gpu/muon.rs).
+int muon_momentum(aur_ctx* ctx, const float* g, float* m, float* upd, size_t n, float beta, bool nesterov);
+int axpby(aur_ctx* ctx, float* out, float alpha, const float* x, float beta, const float* y, size_t n);
+int transpose(aur_ctx* ctx, const float* src, float* dst, int rows, int cols);
+int muon_apply(aur_ctx* ctx, float* p, const float* upd, size_t n, float lr_scale, float lr_wd);
 int scale_by(aur_ctx* ctx, float* x, size_t n, const float* factor);
 int adamw(aur_ctx* ctx, float* p, const float* g, float* m1, float* m2, size_t n, size_t n_decay,
           const float* clip, float lr, float b1, float b2, float eps, float wd, float bc1, float bc2);

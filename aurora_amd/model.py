@@ -88,6 +88,18 @@ class DecoderTransformerGpu:
     def zero_grad(self) -> None:
         self._call("aur_model_zero_grad")
 
+    def step_muon_hybrid(self, muon_lr=0.02, momentum=0.95, nesterov=True, muon_wd=0.0, ns_steps=5,
+                         lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1) -> None:
+        """step_muon_hybrid (model.rs:1023): Muon on the Q/K/V/O/fc/proj
+        matrices, AdamW on embeddings and LayerNorm γ/β."""
+        self._call("aur_model_step_muon_hybrid", muon_lr, momentum, 1 if nesterov else 0, muon_wd,
+                   ns_steps, lr, beta1, beta2, eps, weight_decay)
+
+    def clip_grads_adamw_subset(self, max_norm: float) -> float:
+        n = C.c_float()
+        self._call("aur_model_clip_grads_adamw_subset", max_norm, C.byref(n))
+        return n.value
+
     # ---- AURORA07 checkpoints (src/checkpoint.rs) ----
     def save_checkpoint(self, path, epoch: int = 0, step: int = 0) -> None:
         """checkpoint::save: AURORA07, every optional feature off."""

@@ -231,6 +231,20 @@ int aur_model_clip_grads(aur_model* m, float max_norm, float* norm);
 /* step_adamw (model.rs:926-1009, transformer.rs:2008). */
 int aur_model_step_adamw(aur_model* m, float lr, float beta1, float beta2, float eps,
                          float weight_decay);
+/* step_muon_hybrid (model.rs:1023-1090, gpu/transformer.rs:2052-2291): the
+ * reference trainer's default optimizer.  AdamW (lr, beta1, beta2, eps,
+ * weight_decay; decay on w_tok only) on the embeddings and LayerNorm γ/β;
+ * Muon (muon_lr, momentum, nesterov, muon_wd, ns_steps; optimizer.rs:
+ * 94-305) on every w_q, w_k, w_v, w_o, w_fc, w_proj: momentum, Frobenius
+ * bound, ns_steps quintic Newton–Schulz iterations on the GEMMs, scale
+ * √(max/min).  Shares the AdamW step counter.  The Muon momentum buffers
+ * are allocated (and zeroed) on the first call. */
+int aur_model_step_muon_hybrid(aur_model* m, float muon_lr, float momentum, int32_t nesterov,
+                               float muon_wd, uint32_t ns_steps, float lr, float beta1, float beta2,
+                               float eps, float weight_decay);
+/* clip_grads_adamw_subset (model.rs:1101-1107, gpu/transformer.rs:2294):
+ * the L2 norm and the clip over the AdamW subset only (embeddings + LN). */
+int aur_model_clip_grads_adamw_subset(aur_model* m, float max_norm, float* norm);
 /* clip_grads + step_adamw fused (the clip factor is applied inside AdamW). */
 int aur_model_clip_step_adamw(aur_model* m, float max_norm, float lr, float beta1, float beta2,
                               float eps, float weight_decay, float* norm);

@@ -52,6 +52,8 @@ _SIG = {
     "ora_embed_forward": (None, [_P, _P, _P, _P, _Z, _Z]),
     "ora_embed_backward": (None, [_P, _P, _P, _P, _Z, _Z]),
     "ora_adamw_apply": (None, [_P, _P, _P, _P, _Z, _F, _F, _F, _F, _F, _F, _F, _I]),
+    "ora_newton_schulz5": (None, [_P, _Z, _Z, _P, _I]),
+    "ora_muon_apply": (None, [_P, _P, _P, _Z, _Z, _F, _F, _I, _F, _I, _P]),
     "ora_bias_correction": (None, [_I, _F, _F, C.POINTER(_F), C.POINTER(_F)]),
     "ora_sumsq_acc": (_F, [_P, _Z, _F]),
     "ora_scale": (None, [_P, _Z, _F]),
@@ -289,6 +291,22 @@ def bias_correction(t, beta1, beta2):
     b1, b2 = C.c_float(), C.c_float()
     lib().ora_bias_correction(t, beta1, beta2, C.byref(b1), C.byref(b2))
     return b1.value, b2.value
+
+
+def newton_schulz5(g, rows, cols, n_iter=5) -> None:
+    """In place on the float32 array g (rows × cols, row-major); optimizer.rs:147-252."""
+    m, n = min(rows, cols), max(rows, cols)
+    scratch = np.zeros(2 * m * m + 2 * m * n, np.float32)
+    lib().ora_newton_schulz5(_p(g), rows, cols, _p(scratch), n_iter)
+
+
+def muon_apply(params, grads, mom, rows, cols, lr=0.02, momentum=0.95, nesterov=True, wd=0.0,
+               ns_steps=5) -> None:
+    """optimizer.rs:259-305 on float32 arrays (params and mom updated in place)."""
+    m, n = min(rows, cols), max(rows, cols)
+    scratch = np.zeros(rows * cols + 2 * m * m + 2 * m * n, np.float32)
+    lib().ora_muon_apply(_p(params), _p(grads), _p(mom), rows, cols, lr, momentum, 1 if nesterov else 0,
+                         wd, ns_steps, _p(scratch))
 
 
 def adamw_apply(params, grads, m1, m2, lr, beta1, beta2, eps, wd, bc1, bc2, apply_wd) -> None:

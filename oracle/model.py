@@ -223,6 +223,59 @@ def step_adamw(P, G, state, lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.1) ->
         O.adamw_apply(p, g, m1, m2, lr, beta1, beta2, eps, wd, bc1, bc2, decay)
 
 
+# ------------------------------------------------------------ Muon hybrid
+MUON_SHAPES = (("w_q", "d", "d"), ("w_k", "d", "d"), ("w_v", "d", "d"), ("w_o", "d", "d"),
+               ("w_fc", "d", "F"), ("w_proj", "F", "d"))  # rows × cols as gpu/transformer.rs:858-865 passes them
+
+
+def new_muon_state(P):
+    return [{k: np.zeros_like(L[k]) for k, _, _ in MUON_SHAPES} for L in P["layers"]]
+
+
+def _adamw_subset(G):
+    """The AdamW-managed tensors in model.rs:518-560 order (embeddings, per
+    block LN1 γ/β and LN2 γ/β, final LN)."""
+    yield "w_tok", -1, G["w_tok"]
+    yield "w_pos", -1, G["w_pos"]
+    for l, L in enumerate(G["layers"]):
+        for k in ("ln1_g", "ln1_b", "ln2_g", "ln2_b"):
+            yield k, l, L[k]
+    yield "lnf_g", -1, G["lnf_g"]
+    yield "lnf_b", -1, G["lnf_b"]
+
+
+def clip_grads_adamw_subset(G, max_norm: float) -> float:
+    """model.rs:1101-1107 with l2_norm_adamw_subset :518-560 (one sequential
+    fp32 sum) and scale_adamw_subset :571-..."""
+    s = 0.0
+    for _, _, g in _adamw_subset(G):
+        s = O.sumsq_acc(g, s)
+    n = float(np.sqrt(np.float32(s)))
+    if n > max_norm and n > 0.0:
+        f = np.float32(max_norm) / np.float32(n)
+        for _, _, g in _adamw_subset(G):
+            O.scale_(g, f)
+    return n
+
+
+def step_muon_hybrid(P, G, adam_state, muon_state, cfg: Config, muon_lr=0.02, momentum=0.95, nesterov=True,
+                     muon_wd=0.0, ns_steps=5, lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.1) -> None:
+    """model.rs:1023-1090: shared step counter; AdamW on the embeddings (w_tok
+    decayed, embed_lr_mult = 1) and LayerNorm γ/β; muon_apply on every block
+    matrix with the reference's rows × cols."""
+    adam_state["step"] += 1
+    bc1, bc2 = O.bias_correction(adam_state["step"], beta1, beta2)
+    for (name, l, p), (_, _, g) in zip(_adamw_subset(P), _adamw_subset(G)):
+        m1 = adam_state["m1"][name] if l < 0 else adam_state["m1"]["layers"][l][name]
+        m2 = adam_state["m2"][name] if l < 0 else adam_state["m2"]["layers"][l][name]
+        O.adamw_apply(p, g, m1, m2, lr, beta1, beta2, eps, wd, bc1, bc2, name == "w_tok")
+    dims = {"d": cfg.d_model, "F": cfg.d_ff}
+    for l, L in enumerate(P["layers"]):
+        for k, r, c in MUON_SHAPES:
+            O.muon_apply(L[k], G["layers"][l][k], muon_state[l][k], dims[r], dims[c], muon_lr, momentum,
+                         nesterov, muon_wd, ns_steps)
+
+
 # --------------------------------------------------------------- KV decode
 class KvCache:
     """KvCache (kv_cache.rs:45-92): per-layer K/V rows of one sequence."""

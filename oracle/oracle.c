@@ -462,6 +462,85 @@ void ora_bias_correction(int t, float beta1, float beta2, float* bc1, float* bc2
   *bc2 = 1.0f - powi_f(beta2, t);
 }
 
+/* newton_schulz5 — src/optimizer.rs:147-252: Frobenius bound (skip when
+ * ‖g‖² <= 1e-30), wide orientation [m × n] (physical transpose when
+ * rows > cols), n_iter quintic steps A = X·Xᵀ (upper triangle, mirrored),
+ * B = c·A·A + b·A, X' = a·X + B·X, each sum sequential in k; then back.
+ * scratch: 2·m·m + 2·m·n floats. */
+void ora_newton_schulz5(float* g, size_t rows, size_t cols, float* scratch, int n_iter) {
+  size_t m = rows < cols ? rows : cols, n = rows < cols ? cols : rows;
+  float frob_sq = 0.0f;
+  for (size_t i = 0; i < rows * cols; ++i) frob_sq += g[i] * g[i];
+  if (frob_sq <= 1e-30f) return;
+  float inv_scale = 1.0f / (sqrtf(frob_sq) + 1e-7f);
+  for (size_t i = 0; i < rows * cols; ++i) g[i] *= inv_scale;
+  float* a_buf = scratch;
+  float* b_buf = a_buf + m * m;
+  float* buf_x = b_buf + m * m;
+  float* buf_y = buf_x + m * n;
+  int transposed = rows > cols;
+  if (transposed) {
+    for (size_t r = 0; r < rows; ++r)
+      for (size_t c = 0; c < cols; ++c) buf_x[c * rows + r] = g[r * cols + c];
+  } else {
+    memcpy(buf_x, g, sizeof(float) * m * n);
+  }
+  const float a_coef = 3.4445f, b_coef = -4.7750f, c_coef = 2.0315f;
+  float* cur = buf_x;
+  float* nxt = buf_y;
+  for (int it = 0; it < n_iter; ++it) {
+    for (size_t i = 0; i < m; ++i)
+      for (size_t j = i; j < m; ++j) {
+        float s = 0.0f;
+        for (size_t k = 0; k < n; ++k) s += cur[i * n + k] * cur[j * n + k];
+        a_buf[i * m + j] = s;
+        if (i != j) a_buf[j * m + i] = s;
+      }
+    for (size_t i = 0; i < m; ++i)
+      for (size_t j = 0; j < m; ++j) {
+        float s = 0.0f;
+        for (size_t k = 0; k < m; ++k) s += a_buf[i * m + k] * a_buf[k * m + j];
+        b_buf[i * m + j] = c_coef * s + b_coef * a_buf[i * m + j];
+      }
+    for (size_t i = 0; i < m; ++i)
+      for (size_t j = 0; j < n; ++j) {
+        float s = 0.0f;
+        for (size_t k = 0; k < m; ++k) s += b_buf[i * m + k] * cur[k * n + j];
+        nxt[i * n + j] = a_coef * cur[i * n + j] + s;
+      }
+    float* t = cur;
+    cur = nxt;
+    nxt = t;
+  }
+  if (transposed) {
+    for (size_t r = 0; r < rows; ++r)
+      for (size_t c = 0; c < cols; ++c) g[r * cols + c] = cur[c * rows + r];
+  } else {
+    memcpy(g, cur, sizeof(float) * m * n);
+  }
+}
+
+/* muon_apply — src/optimizer.rs:259-305: momentum (Nesterov lookahead),
+ * newton_schulz5, spectral scale √(max/min), decoupled decay.
+ * scratch: rows·cols + 2·m·m + 2·m·n floats. */
+void ora_muon_apply(float* params, const float* grads, float* mom, size_t rows, size_t cols, float lr,
+                    float momentum, int nesterov, float weight_decay, int ns_steps, float* scratch) {
+  size_t n_el = rows * cols;
+  float* update = scratch;
+  for (size_t i = 0; i < n_el; ++i) {
+    mom[i] = momentum * mom[i] + grads[i];
+    update[i] = nesterov ? grads[i] + momentum * mom[i] : mom[i];
+  }
+  ora_newton_schulz5(update, rows, cols, scratch + n_el, ns_steps);
+  size_t m = rows < cols ? rows : cols, n = rows < cols ? cols : rows;
+  float scale = sqrtf((float)n / (float)m);
+  for (size_t i = 0; i < n_el; ++i) {
+    float step = lr * scale * update[i];
+    if (weight_decay > 0.0f) step += lr * weight_decay * params[i];
+    params[i] -= step;
+  }
+}
+
 /* ModelGrads::l2_norm's per-tensor term — src/transformer/model.rs:442-500:
  * one fp32 accumulator s += v·v carried across tensors in a fixed order. */
 float ora_sumsq_acc(const float* x, size_t n, float s) {
