@@ -67,6 +67,8 @@ SIGNATURES: dict[str, tuple] = {
     "aur_model_train_step_batch": (_i32, [C.c_void_p, C.c_void_p, C.c_void_p, _u32, _u32,
                                           C.POINTER(C.c_float)]),
     "aur_model_forward": (_i32, [C.c_void_p, C.c_void_p, _u32, _u32, C.c_void_p]),
+    "aur_model_eval_step_batch": (_i32, [C.c_void_p, C.c_void_p, C.c_void_p, _u32, _u32,
+                                         C.c_void_p]),
     "aur_model_clip_grads": (_i32, [C.c_void_p, C.c_float, C.POINTER(C.c_float)]),
     "aur_model_step_adamw": (_i32, [C.c_void_p, C.c_float, C.c_float, C.c_float, C.c_float,
                                     C.c_float]),

@@ -223,6 +223,12 @@ class DecoderTransformerGpu {
   float train_step_batch(const uint32_t* tokens, const uint32_t* targets, uint32_t b, uint32_t t);
   // Forward only; logits [b·t, vocab] to the host if non-null.
   void forward(const uint32_t* tokens, uint32_t b, uint32_t t, float* logits_host);
+  // Forward + softmax-CE with loss scale 1 and no backward: per-token NLL in
+  // nats for b windows of length t into nll_host [b·t] (window-major).
+  // Parameters, gradients and optimizer moments are not touched
+  // (src/gpu/transformer.rs:1723-1811).
+  void eval_step_batch(const uint32_t* tokens, const uint32_t* targets, uint32_t b, uint32_t t,
+                       float* nll_host);
   // model.rs:1011-1017: global L2 norm over all grads, scaled in place when
   // above max_norm; returns the pre-clip norm.
   float clip_grads(float max_norm);

@@ -392,6 +392,20 @@ void DecoderTransformerGpu::forward(const uint32_t* tokens, uint32_t b, uint32_t
     ck(ctx_, aur_d2h(ctx_, logits_host, acts_->logits, (size_t)b * t * cfg_.vocab * 4), "download logits");
 }
 
+void DecoderTransformerGpu::eval_step_batch(const uint32_t* tokens, const uint32_t* targets, uint32_t b,
+                                            uint32_t t, float* nll_host) {
+  if (b == 0 || t == 0) return;
+  if (b > max_batch_ || t > cfg_.seq_len_max) throw Error("eval_step_batch: batch/seq too large", AUR_ELIMIT);
+  auto& A = *acts_;
+  const size_t M = (size_t)b * t;
+  upload_tokens(tokens, targets, b, t);
+  encode_forward(b, t, nullptr, true);
+  // The logits arena takes the (unused) softmax gradient in place; the NLL
+  // rows are exact log-sum-exp minus the target logit, independent of scale.
+  ck(ctx_, aur::softmax_ce(ctx_, A.logits, A.tgt, A.nll, (int)M, (int)cfg_.vocab, 1.0f), "softmax_ce");
+  ck(ctx_, aur_d2h(ctx_, nll_host, A.nll, M * 4), "download nll");
+}
+
 float DecoderTransformerGpu::clip_grads(float max_norm) {
   auto& A = *acts_;
   ck(ctx_, aur::grad_norm(ctx_, grads_, n_params_, max_norm, A.norm_part, A.stats), "grad norm");
@@ -859,6 +873,12 @@ int aur_model_train_step_batch(aur_model* m, const uint32_t* tokens, const uint3
 int aur_model_forward(aur_model* m, const uint32_t* tokens, uint32_t b, uint32_t t, float* logits) {
   if (!m || !tokens) return AUR_EINVAL;
   return guard(m->m->ctx(), [&] { m->m->forward(tokens, b, t, logits); });
+}
+
+int aur_model_eval_step_batch(aur_model* m, const uint32_t* tokens, const uint32_t* targets, uint32_t b,
+                              uint32_t t, float* nll) {
+  if (!m || !tokens || !targets || !nll) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] { m->m->eval_step_batch(tokens, targets, b, t, nll); });
 }
 
 int aur_model_clip_grads(aur_model* m, float max_norm, float* norm) {

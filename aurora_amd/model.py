@@ -135,6 +135,35 @@ class DecoderTransformerGpu:
         self._call("aur_model_forward", tok.ctypes.data, b, t, out.ctypes.data if want_logits else None)
         return out
 
+    def eval_step_batch(self, inputs, targets) -> np.ndarray:
+        """Per-token NLL (nats) of b equal-length windows, flat [b·t]
+        window-major; the caller slices per window
+        (src/gpu/transformer.rs:1734-1775).  No gradient or optimizer state
+        is touched."""
+        if len(inputs) != len(targets):
+            raise ValueError("eval_step_batch: inputs and targets differ in window count")
+        if len(inputs) == 0:
+            return np.empty(0, np.float32)
+        tok, tgt = _u32(inputs), _u32(targets)
+        if tok.ndim != 2 or tok.shape != tgt.shape:
+            raise ValueError("eval_step_batch: windows must all have one length, targets the same shape")
+        b, t = tok.shape
+        out = np.empty(b * t, np.float32)
+        self._call("aur_model_eval_step_batch", tok.ctypes.data, tgt.ctypes.data, b, t, out.ctypes.data)
+        return out
+
+    def eval_step_per_token(self, tokens, targets) -> np.ndarray:
+        """Per-position NLL of one window (src/gpu/transformer.rs:1779-1811)."""
+        return self.eval_step_batch([tokens], [targets])
+
+    def eval_step(self, tokens, targets) -> float:
+        """Sum of the window's per-token NLL (src/gpu/transformer.rs:1723-1725);
+        summed in f32 in position order like the reference's iterator sum."""
+        s = np.float32(0.0)
+        for x in self.eval_step_per_token(tokens, targets):
+            s = np.float32(s + x)
+        return float(s)
+
     def clip_grads(self, max_norm: float) -> float:
         n = C.c_float()
         self._call("aur_model_clip_grads", max_norm, C.byref(n))

@@ -30,9 +30,9 @@ PEAK_HBM = 8000.0       # GB/s
 
 COPY_MIB = 256          # calibration copy of the --only traffic leg
 # HBM bytes per head-GEMM launch from the two counter passes of
-# profiles/gemm_head_nt_8192x8192x512_traffic.md: FETCH_SIZE 133169.8 KiB × 2.000
-# + WRITE_SIZE 292192.8 KiB × 1.000 (factors from the 256 MiB copy).
-HEAD_TRAFFIC_BYTES = (133169.8 * 2.000 + 292192.8 * 1.000) * 1024
+# profiles/gemm_head_nt_8192x8192x512_traffic.md: FETCH_SIZE 158034.0 KiB × 2.000
+# + WRITE_SIZE 262144.8 KiB × 1.000 (factors from the 256 MiB copy).
+HEAD_TRAFFIC_BYTES = (158034.0 * 2.000 + 262144.8 * 1.000) * 1024
 SWEEP_KN = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
 M = 8192
 

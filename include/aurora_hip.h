@@ -225,6 +225,13 @@ int aur_model_train_step_batch(aur_model* m, const uint32_t* tokens, const uint3
 /* Forward only (encode_forward, transformer.rs:1347); logits [b*t, vocab]
  * copied to the host buffer `logits` when non-NULL. */
 int aur_model_forward(aur_model* m, const uint32_t* tokens, uint32_t b, uint32_t t, float* logits);
+/* eval_step_batch (transformer.rs:1734-1775; eval_step_per_token :1779-1811
+ * is the b = 1 case, eval_step :1723 its sum): forward + softmax-CE at loss
+ * scale 1, no backward, for b windows of length t (tokens/targets [b*t]);
+ * nll[b*t] receives the per-token NLL in nats, window-major.  Parameters,
+ * gradients and optimizer state are left untouched. */
+int aur_model_eval_step_batch(aur_model* m, const uint32_t* tokens, const uint32_t* targets,
+                              uint32_t b, uint32_t t, float* nll);
 /* clip_grads (model.rs:1011-1017): global L2 over all gradients, scaled in
  * place when above max_norm; *norm = the pre-clip norm. */
 int aur_model_clip_grads(aur_model* m, float max_norm, float* norm);

@@ -49,6 +49,7 @@ _SIG = {
     "ora_gelu": (None, [_P, _P, _Z]),
     "ora_gelu_backward": (None, [_P, _P, _Z]),
     "ora_softmax_ce": (_F, [_P, _P, _P, _Z, _Z]),
+    "ora_token_nll": (None, [_P, _P, _P, _Z, _Z]),
     "ora_embed_forward": (None, [_P, _P, _P, _P, _Z, _Z]),
     "ora_embed_backward": (None, [_P, _P, _P, _P, _Z, _Z]),
     "ora_adamw_apply": (None, [_P, _P, _P, _P, _Z, _F, _F, _F, _F, _F, _F, _F, _I]),
@@ -273,6 +274,15 @@ def softmax_ce(logits, targets, v):
     d = np.empty(t * v, np.float32)
     total = lib().ora_softmax_ce(_p(logits), _p(targets), _p(d), t, v)
     return float(total), d
+
+
+def token_nll(logits, targets, v) -> np.ndarray:
+    """Per-token NLL [t] without a gradient (src/gpu/softmax_ce.rs:101-102)."""
+    logits, targets = f32(logits), u32(targets)
+    t = targets.size
+    out = np.empty(t, np.float32)
+    lib().ora_token_nll(_p(logits), _p(targets), _p(out), t, v)
+    return out
 
 
 def embed_forward(w_tok, w_pos, tokens, d) -> np.ndarray:

@@ -413,6 +413,23 @@ float ora_softmax_ce(const float* logits, const uint32_t* targets, float* d_logi
   return total;
 }
 
+/* Per-token NLL in nats without a gradient: the loss_seq row the GPU
+ * softmax-CE writes, -ln(max(p_target, 1e-12)) (src/gpu/softmax_ce.rs:101-102;
+ * the CPU eval's logsumexp form, examples/aurora_train.rs:1713-1719, is the
+ * same quantity with the clamp at ln 1e-12 = -27.631021). */
+void ora_token_nll(const float* logits, const uint32_t* targets, float* nll, size_t t, size_t v) {
+  for (size_t ti = 0; ti < t; ++ti) {
+    const float* row = logits + ti * v;
+    float mx = -INFINITY;
+    for (size_t c = 0; c < v; ++c) mx = fmaxf(mx, row[c]);
+    float sum = 0.0f;
+    for (size_t c = 0; c < v; ++c) sum += expf(row[c] - mx);
+    float pt = expf(row[targets[ti]] - mx) / sum;
+    if (pt < 1e-12f) pt = 1e-12f;
+    nll[ti] = -logf(pt);
+  }
+}
+
 /* embed_forward / embed_backward — src/transformer/embedding.rs:95-142. */
 void ora_embed_forward(const float* w_tok, const float* w_pos, const uint32_t* tokens, float* out,
                        size_t t, size_t d) {
