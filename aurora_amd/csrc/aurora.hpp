@@ -266,6 +266,7 @@ class DecoderTransformerGpu {
   struct Acts;
   void encode_forward(uint32_t b, uint32_t t, KvCacheGpu* cache, bool head_all_rows);
   void encode_decode_step(KvCacheGpu& cache);
+  void ensure_decode_graph(KvCacheGpu& cache);
   void encode_backward(uint32_t b, uint32_t t);
   void upload_tokens(const uint32_t* tokens, const uint32_t* targets, uint32_t b, uint32_t t);
 

@@ -618,7 +618,36 @@ void DecoderTransformerGpu::prefill_kv(KvCacheGpu& cache, const uint32_t* tokens
   std::vector<int32_t> pos(b, (int32_t)t);
   ck(ctx_, aur_h2d(ctx_, cache.pos_, pos.data(), b * 4), "prefill pos");
   cache.current_len = t;
+  ensure_decode_graph(cache);
   if (last_logits) ck(ctx_, aur_d2h(ctx_, last_logits, cache.logits_, (size_t)b * V * 4), "download logits");
+}
+
+// One decode step is ~90 small launches: it is captured once per cache as a
+// HIP graph (all pointers and shapes are fixed per cache; positions live on
+// the device) and replayed, so the host issues one launch per step.  The
+// capture is done by prefill_kv, so the first generate_step does not pay for
+// it; a cache that was never prefilled captures on first use.
+void DecoderTransformerGpu::ensure_decode_graph(KvCacheGpu& cache) {
+  if (cache.graph_ || cache.batch > 64) return;
+  hipStream_t st = static_cast<hipStream_t>(aur_stream(ctx_));
+  if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess)
+    throw Error("decode graph: hipStreamBeginCapture failed", AUR_EINVAL);
+  try {
+    encode_decode_step(cache);
+  } catch (...) {
+    hipGraph_t g = nullptr;
+    hipStreamEndCapture(st, &g);
+    if (g) hipGraphDestroy(g);
+    throw;
+  }
+  hipGraph_t g = nullptr;
+  if (hipStreamEndCapture(st, &g) != hipSuccess || !g)
+    throw Error("decode graph: hipStreamEndCapture failed", AUR_EINVAL);
+  hipGraphExec_t ex = nullptr;
+  const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) throw Error("decode graph: hipGraphInstantiate failed", (int)e);
+  cache.graph_ = ex;
 }
 
 void DecoderTransformerGpu::generate_step_kv(KvCacheGpu& cache, const uint32_t* tokens, float* logits_host,
@@ -632,29 +661,7 @@ void DecoderTransformerGpu::generate_step_kv(KvCacheGpu& cache, const uint32_t* 
   }
   hipStream_t st = static_cast<hipStream_t>(aur_stream(ctx_));
   if (cache.batch <= 64) {
-    // One decode step is ~100 small launches: capture it once as a HIP graph
-    // (all pointers and shapes are fixed per cache; positions live on the
-    // device) and replay it, so the host issues one launch per step.
-    if (!cache.graph_) {
-      if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess)
-        throw Error("generate_step_kv: hipStreamBeginCapture failed", AUR_EINVAL);
-      try {
-        encode_decode_step(cache);
-      } catch (...) {
-        hipGraph_t g = nullptr;
-        hipStreamEndCapture(st, &g);
-        if (g) hipGraphDestroy(g);
-        throw;
-      }
-      hipGraph_t g = nullptr;
-      if (hipStreamEndCapture(st, &g) != hipSuccess || !g)
-        throw Error("generate_step_kv: hipStreamEndCapture failed", AUR_EINVAL);
-      hipGraphExec_t ex = nullptr;
-      const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-      hipGraphDestroy(g);
-      if (e != hipSuccess) throw Error("generate_step_kv: hipGraphInstantiate failed", (int)e);
-      cache.graph_ = ex;
-    }
+    ensure_decode_graph(cache);
     const hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(cache.graph_), st);
     if (e != hipSuccess) throw Error(std::string("hipGraphLaunch: ") + hipGetErrorString(e), (int)e);
   } else {

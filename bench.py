@@ -166,7 +166,8 @@ def bench_decode(ctx, n_steps: int = 256) -> dict:
     m.prefill_kv(cache, prompts)
     e1.record()
     prefill_ms = e0.elapsed_ms(e1)
-    # warm the decode path on a scratch cache, then time the real run
+    # prefill_kv also captured the decode-step graph (its cost is in
+    # prefill_ms); the timed region is the n_steps graph replays
     ctx.sync()
     e0.record()
     m.generate_greedy(cache, n_steps, collect=False)
