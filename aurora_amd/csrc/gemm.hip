@@ -626,6 +626,73 @@ __global__ void __launch_bounds__(256) wide_partials_kernel(GemmArgs g) {
   }
 }
 
+// ------------------------------------ decode K-range partials, short ranges
+// P[z][M ≤ 16·MT][N] for K range z of KR (64 or 128) and N % 64 == 0.  A
+// 256-thread block owns 64 columns (16 per wave) and one range.  Each wave
+// issues every W load of its 16 rows × KR first (coalesced: lanes 4r..4r+3
+// read row r's 64 contiguous bytes per 16-k chunk, moved into the MFMA
+// layout with ds_bpermute), the X slice [M][KR] goes to LDS once for the
+// four waves, then the MFMAs run as the W chunks land.  With these short
+// ranges a CU holds three or more blocks, so the X bytes each CU reads stay
+// below its W bytes — the full-K skinny kernel reads all of X per 16
+// columns, twice its W bytes at K = 1024.
+template <int MT, int KR>
+__global__ void __launch_bounds__(256) stream_partials_kernel(GemmArgs g) {
+  constexpr int XR = 16 * MT, LDX = KR + 4, NC = KR / 16;
+  constexpr int XPT = XR * KR / 4 / 256;  // float4 of the X slice per thread
+  static_assert(XPT >= 1 && XR * KR % 1024 == 0, "X slice/threads mismatch");
+  __shared__ __attribute__((aligned(16))) float xs[XR * LDX];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g16 = lane >> 4, l16 = lane & 15;
+  const int lr = lane >> 2, lk = (lane & 3) * 4;
+  const int perm = 4 * (4 * l16 + g16);
+  const int n0 = blockIdx.x * 64 + 16 * w;
+  const int kb = blockIdx.y * KR;
+  floatx4 xr[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int f = tid + 256 * i, r = f / (KR / 4), c = (f % (KR / 4)) * 4;
+    // rows past M read row 0 (in bounds) and stage zeros
+    const floatx4 v = *reinterpret_cast<const floatx4*>(g.A + (size_t)(r < g.M ? r : 0) * g.lda + kb + c);
+    xr[i] = r < g.M ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  floatx4 wf[NC];
+  const float* wrow = g.B + (size_t)(n0 + lr) * g.ldb + kb + lk;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) wf[c] = *reinterpret_cast<const floatx4*>(wrow + 16 * c);
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int f = tid + 256 * i, r = f / (KR / 4), c = (f % (KR / 4)) * 4;
+    *reinterpret_cast<floatx4*>(xs + r * LDX + c) = xr[i];
+  }
+  __syncthreads();
+  floatx4 acc[MT], acc2[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = acc2[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const floatx4 wz = to_mfma_layout(wf[c], perm);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const floatx4 xf = *reinterpret_cast<const floatx4*>(xs + (16 * i + l16) * LDX + 16 * c + 4 * g16);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (c & 1)
+          acc2[i] = mfma16x16x4(xf[s], wz[s], acc2[i]);
+        else
+          acc[i] = mfma16x16x4(xf[s], wz[s], acc[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = 16 * i + 4 * g16 + e;
+      if (row < g.M) g.P[((size_t)blockIdx.y * g.M + row) * g.N + n0 + l16] = acc[i][e] + acc2[i][e];
+    }
+}
+
 struct Plan {
   int bm, bn, splits, k_chunk;
 };
@@ -887,6 +954,26 @@ int gemm_nt_partials(aur_ctx* ctx, const float* A, int lda, const float* B, int 
   a.A = A; a.B = B; a.P = P; a.M = M; a.N = N; a.K = K;
   a.lda = lda; a.ldb = ldb; a.k_chunk = chunk;
   dim3 grid((N + 63) / 64, splits);
+  if ((chunk == 64 || chunk == 128) && N % 64 == 0 && K % chunk == 0) {
+#define AUR_STREAM_PARTIALS(MT)                                                                  \
+  do {                                                                                            \
+    if (chunk == 64)                                                                              \
+      hipLaunchKernelGGL((stream_partials_kernel<MT, 64>), grid, dim3(256), 0, ctx->stream, a);  \
+    else                                                                                          \
+      hipLaunchKernelGGL((stream_partials_kernel<MT, 128>), grid, dim3(256), 0, ctx->stream, a); \
+  } while (0)
+    if (M <= 16)
+      AUR_STREAM_PARTIALS(1);
+    else if (M <= 32)
+      AUR_STREAM_PARTIALS(2);
+    else if (M <= 48)
+      AUR_STREAM_PARTIALS(3);
+    else
+      AUR_STREAM_PARTIALS(4);
+#undef AUR_STREAM_PARTIALS
+    AUR_LAUNCH_CHECK(ctx, "stream_partials_kernel");
+    return 0;
+  }
   if (M <= 16)
     hipLaunchKernelGGL(wide_partials_kernel<1>, grid, dim3(256), 0, ctx->stream, a);
   else if (M <= 32)

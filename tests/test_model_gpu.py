@@ -231,3 +231,49 @@ def test_config3_shape_train_step_runs(ctx):
     norm = m.clip_step_adamw(1.0, lr=3e-4, weight_decay=0.1)
     assert np.isfinite(norm) and norm > 0
     m.destroy()
+
+
+def test_config4_decode_equals_full_forward(ctx):
+    """Full config-4 shapes (the config-3 model, 32 prompts × 512, fp32 KV):
+    every decode step's logits equal the last-position logits of a full
+    forward (a fresh prefill) over the same grown sequences — the size-free
+    form of kv_cache.rs:166-213 — and the greedy tokens agree wherever the
+    top-2 logit gap exceeds the comparison noise."""
+    C3 = dict(vocab=8192, d_model=1024, n_layer=12, n_head=16, d_ff=4096, seq_len_max=1024)
+    from aurora_amd.model import DecoderTransformerGpu
+
+    B, T0, steps = 32, 512, 6
+    m = DecoderTransformerGpu(ctx, max_batch=B, **C3)
+    rng = np.random.default_rng(2)
+    m.set("params", rng.standard_normal(m.tensor_ptr("params")[1], dtype=np.float32) * np.float32(0.02))
+    res = np.float32(1.0 / np.sqrt(2.0 * 12))
+    for l in range(12):
+        m.set("w_o", m.get("w_o", l) * res, l)
+        m.set("w_proj", m.get("w_proj", l) * res, l)
+        for k in ("ln1_g", "ln2_g"):
+            m.set(k, np.ones(1024, np.float32), l)
+        for k in ("ln1_b", "ln2_b"):
+            m.set(k, np.zeros(1024, np.float32), l)
+    m.set("lnf_g", np.ones(1024, np.float32))
+    m.set("lnf_b", np.zeros(1024, np.float32))
+    prompts = rng.integers(0, 8192, (B, T0)).astype(np.uint32)
+    cache = m.kv_cache(B, T0 + steps + 1)
+    ref = m.kv_cache(B, T0 + steps + 1)
+    last = m.prefill_kv(cache, prompts)
+    seq = np.concatenate([prompts, last.argmax(1).astype(np.uint32)[:, None]], axis=1)
+    worst, ties = 0.0, 0
+    for s in range(steps):
+        logits, nxt = m.generate_step_kv(cache)  # feeds the previous argmax
+        full = m.prefill_kv(ref, seq)  # full forward over the grown sequences
+        e = fro_rel(logits, full)
+        worst = max(worst, e)
+        assert e < 1e-4, (s, e)
+        order = np.sort(full, axis=1)
+        clear = (order[:, -1] - order[:, -2]) > 1e-3
+        ties += int((~clear).sum())
+        assert np.array_equal(nxt[clear], full.argmax(1)[clear]), s
+        seq = np.concatenate([seq, nxt[:, None]], axis=1)
+    print(f"[config4] {steps} steps x {B} seqs: max rel |kv - full| {worst:.2e}, near ties skipped {ties}")
+    cache.destroy()
+    ref.destroy()
+    m.destroy()
