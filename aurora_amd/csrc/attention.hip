@@ -8,10 +8,13 @@
 // Instead of materialising P ([H,T,T] in the reference) the forward keeps
 // the running row max / row sum of a flash-style tile loop and stores one
 // log-sum-exp per row; the backward recomputes P tile by tile from it.
-// rowdot_i equals Σ_c dO_ic O_ic, computed once per row (pass 1).  dQ is
-// produced by a pass over key tiles (pass 2) and dK/dV by a pass over query
-// tiles (pass 3), so every output element has exactly one writer: the
-// backward is deterministic, like the reference's 3-dispatch scheme.
+// rowdot_i equals Σ_c dO_ic O_ic, computed once per row (pass 1).  dK/dV
+// come from a pass over query tiles per key tile (pass 2), which also stores
+// each dS tile of the causal lower triangle to the workspace; dQ = dS·K is
+// then a pass over those tiles per query tile (pass 3) that reads dS instead
+// of recomputing S and dP.  Every output element has exactly one writer and
+// a fixed summation order: the backward is deterministic, like the
+// reference's 3-dispatch scheme (whose d_scores scratch is [H,T,T]).
 //
 // MFMA layout (v_mfma_f32_16x16x4_f32, see common.hpp).  A wave owns 16 rows
 // (queries in the forward and dQ pass, keys in the dK/dV pass).  Scores are
@@ -38,6 +41,8 @@ struct AttnArgs {
   float* out;        // forward output
   float* lse;        // [B, H, T]
   float* D;          // [B, H, T] rowdot
+  float* ds;         // [B, H, ntri, 64, 64] dS tiles of the causal lower triangle
+  int ntri;          // nqt·(nqt+1)/2 tiles per (sequence, head)
   float* dq;
   float* dk;
   float* dv;
@@ -276,111 +281,7 @@ __global__ void __launch_bounds__(256) mha_bwd_rowdot_kernel(AttnArgs a, int B) 
   }
 }
 
-// ---------------------------------------------------- backward pass 2: dQ
-// One 64-key tile of dQᵀ for this lane's query row.  Only the diagonal tile
-// (DIAG) is masked; keys past T only occur there and their K/V rows are zero.
-template <int DH, bool DIAG>
-__device__ __forceinline__ void dq_tile(const float* __restrict__ Ks, const float* __restrict__ Vs,
-                                        const floatx4* qf, const floatx4* df, floatx4* acc, float lse2,
-                                        float Dq, int w, int g, int l16) {
-  using G = Geo<DH>;
-  constexpr int NC = G::NC, LDT = G::LDT;
-  const int jmax = DIAG ? w : 3;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (j > jmax) continue;
-    floatx4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const floatx4 kf = *reinterpret_cast<const floatx4*>(Ks + (16 * j + l16) * LDT + 16 * c + 4 * g);
-      const floatx4 vf = *reinterpret_cast<const floatx4*>(Vs + (16 * j + l16) * LDT + 16 * c + 4 * g);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        st = mfma16x16x4(kf[s], qf[c][s], st);  // Sᵀ[key][q] (log2 domain)
-        dp = mfma16x16x4(vf[s], df[c][s], dp);  // dPᵀ[key][q]
-      }
-    }
-    // dSᵀ = Pᵀ ⊙ (dPᵀ − D_q)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float p = __builtin_amdgcn_exp2f(st[e] - lse2);
-      if (DIAG && 16 * j + 4 * g + e > 16 * w + l16) p = 0.f;
-      st[e] = p * (dp[e] - Dq);
-    }
-    // dQᵀ[d][q] += Kᵀ[d][key] · dSᵀ[key][q]
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float* kr = Ks + (16 * j + 4 * g + s) * LDT + l16;
-#pragma unroll
-      for (int d = 0; d < NC; ++d) acc[d] = mfma16x16x4(kr[16 * d], st[s], acc[d]);
-    }
-  }
-}
-
-template <int DH>
-__global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
-  using G = Geo<DH>;
-  constexpr int NC = G::NC;
-  __shared__ __attribute__((aligned(16))) float sm[2][G::TILE];  // [K,V]
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int g = lane >> 4, l16 = lane & 15;
-  const int nqt = (a.T + TQ - 1) / TQ;
-  const int qt = nqt - 1 - blockIdx.z;  // longest query tiles first (grid H, B, tiles)
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int q0 = qt * TQ;
-  const size_t row_base = (size_t)b * a.T;
-  const float* Qb = a.q + row_base * a.ld_qkv + h * DH;
-  const float* Kb = a.k + row_base * a.ld_qkv + h * DH;
-  const float* Vb = a.v + row_base * a.ld_qkv + h * DH;
-  const float* dOb = a.dO + row_base * a.ld_o + h * DH;
-
-  const int qrow = q0 + 16 * w + l16;
-  floatx4 qf[NC], df[NC];
-  load_rows_frag<DH>(qf, Qb, a.ld_qkv, qrow, a.T, g);
-  load_rows_frag<DH>(df, dOb, a.ld_o, qrow, a.T, g);
-  const float sl2 = a.scale * LOG2E;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) qf[c] *= sl2;
-  const size_t stat = ((size_t)b * a.H + h) * a.T;
-  const float lse2 = qrow < a.T ? a.lse[stat + qrow] * LOG2E : 0.f;
-  const float Dq = qrow < a.T ? a.D[stat + qrow] : 0.f;
-
-  floatx4 acc[NC];
-#pragma unroll
-  for (int d = 0; d < NC; ++d) acc[d] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  zero_pad_cols<DH>(sm[0], tid);
-  zero_pad_cols<DH>(sm[1], tid);
-  TileRegs<DH> rk, rv;
-  rk.load(Kb, a.ld_qkv, 0, a.T, tid);
-  rv.load(Vb, a.ld_qkv, 0, a.T, tid);
-  rk.store(sm[0], tid);
-  rv.store(sm[1], tid);
-  __syncthreads();
-
-  for (int kt = 0; kt < qt; ++kt) {
-    rk.load(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
-    rv.load(Vb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
-    dq_tile<DH, false>(sm[0], sm[1], qf, df, acc, lse2, Dq, w, g, l16);
-    __syncthreads();  // every wave is done with the stage
-    rk.store(sm[0], tid);
-    rv.store(sm[1], tid);
-    __syncthreads();
-  }
-  dq_tile<DH, true>(sm[0], sm[1], qf, df, acc, lse2, Dq, w, g, l16);
-
-  if (qrow < a.T) {
-    float* dqr = a.dq + (row_base + qrow) * a.ld_d + h * DH;
-#pragma unroll
-    for (int d = 0; d < NC; ++d) {
-      if (!G::live(16 * d + 4 * g)) continue;
-      floatx4* p = reinterpret_cast<floatx4*>(dqr + 16 * d + 4 * g);
-      *p = *p + acc[d] * a.scale;
-    }
-  }
-}
-
-// ------------------------------------------------- backward pass 3: dK, dV
+// ---------------------------------------- backward pass 2: dK, dV (and dS)
 template <int DH, int NS>
 __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
   using G = Geo<DH>;
@@ -453,6 +354,7 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
     const float* Qs = sm[cur][0];
     const float* dOs = sm[cur][1];
     const int q0 = qt * TQ;
+    float* ds_tile = a.ds + (((size_t)b * a.H + h) * a.ntri + qt * (qt + 1) / 2 + kt) * (TQ * TQ);
     // Query sub-tiles jq < w of the diagonal tile lie entirely before this
     // wave's keys: fully masked.
     const int jmin = (qt == kt) ? w : 0;
@@ -480,6 +382,8 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
         if (qt == kt && krow > q) pe = 0.f;
         p[e] = pe;
         ds[e] = pe * (dp[e] - Dq[e]);
+        // dS tile (qt, kt), row-major [q][key], for the dQ pass
+        ds_tile[(16 * jq + 4 * g + e) * TQ + 16 * w + l16] = ds[e];
       }
       // dVᵀ[d][key] += dOᵀ[d][q]·P[q][key];  dKᵀ[d][key] += Qᵀ[d][q]·dS[q][key]
 #pragma unroll
@@ -518,7 +422,89 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------- backward pass 3: dQ
+// dQ[q] = scale · Σ_key dS[q][key] K[key] over the key tiles 0..qt of this
+// query tile, in increasing key order, from the dS tiles pass 2 stored.  A
+// wave owns 16 query rows; lane l reads dS[16w + l%16][16j + 4·(l/16) .. +3]
+// (one float4 per 16-key sub-tile j), which is exactly the B operand of
+// dQᵀ[d][q] += Kᵀ[d][key]·dSᵀ[key][q] in the Sᵀ layout of the other passes.
+// K tiles go through LDS double-buffered, the next tile's dS fragments are
+// loaded into registers while the current ones are multiplied.  On the
+// diagonal tile only sub-tiles j ≤ w hold keys at or before this wave's
+// queries (pass 2 wrote them, zero where masked); the others are skipped.
+template <int DH>
+__global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
+  using G = Geo<DH>;
+  constexpr int NC = G::NC, LDT = G::LDT;
+  __shared__ __attribute__((aligned(16))) float sm[2][G::TILE];  // K tiles
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int nqt = (a.T + TQ - 1) / TQ;
+  const int qt = nqt - 1 - blockIdx.z;  // longest query tiles first (grid H, B, tiles)
+  const int h = blockIdx.x, b = blockIdx.y;
+  const size_t row_base = (size_t)b * a.T;
+  const float* Kb = a.k + row_base * a.ld_qkv + h * DH;
+  // dS tile (qt, kt) at tiles + kt·TQ², this lane's row and column offset folded in
+  const float* tiles = a.ds + (((size_t)b * a.H + h) * a.ntri + qt * (qt + 1) / 2) * (TQ * TQ) +
+                       (16 * w + l16) * TQ + 4 * g;
+  auto load_ds = [&](int kt, floatx4* f) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[j] = *reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + 16 * j);
+  };
+
+  floatx4 acc[NC];
+#pragma unroll
+  for (int d = 0; d < NC; ++d) acc[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+  zero_pad_cols<DH>(sm[0], tid);
+  zero_pad_cols<DH>(sm[1], tid);
+  TileRegs<DH> rk;
+  floatx4 fc[4], fn[4];
+  rk.load(Kb, a.ld_qkv, 0, a.T, tid);
+  load_ds(0, fc);
+  rk.store(sm[0], tid);
+  __syncthreads();
+  for (int kt = 0; kt <= qt; ++kt) {
+    const bool more = kt < qt;
+    if (more) {
+      rk.load(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, tid);
+      load_ds(kt + 1, fn);
+    }
+    const float* Ks = sm[kt & 1];
+    const int jmax = more ? 3 : w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j > jmax) continue;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float* kr = Ks + (16 * j + 4 * g + s) * LDT + l16;
+#pragma unroll
+        for (int d = 0; d < NC; ++d) acc[d] = mfma16x16x4(kr[16 * d], fc[j][s], acc[d]);
+      }
+    }
+    if (more) {
+      // the other buffer was last read in iteration kt-1, before the barrier
+      rk.store(sm[(kt + 1) & 1], tid);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fc[j] = fn[j];
+      __syncthreads();
+    }
+  }
+  const int qrow = qt * TQ + 16 * w + l16;
+  if (qrow < a.T) {
+    float* dqr = a.dq + (row_base + qrow) * a.ld_d + h * DH;
+#pragma unroll
+    for (int d = 0; d < NC; ++d) {
+      if (!G::live(16 * d + 4 * g)) continue;
+      floatx4* p = reinterpret_cast<floatx4*>(dqr + 16 * d + 4 * g);
+      *p = *p + acc[d] * a.scale;
+    }
+  }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Workspace: rowdot D [B,H,T], padded to 256 bytes, then the dS tiles.
+size_t ws_d_floats(size_t b, size_t t, size_t n_head) { return (b * t * n_head + 63) / 64 * 64; }
 
 bool dh_supported(uint32_t d) { return d == 8 || d == 16 || d == 32 || d == 64; }
 
@@ -547,8 +533,8 @@ void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
   hipLaunchKernelGGL(mha_bwd_rowdot_kernel<DH>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256),
                      0, st, a, b);
   dim3 grid(a.H, b, (a.T + TQ - 1) / TQ);
+  hipLaunchKernelGGL((mha_bwd_dkv_kernel<DH, 2>), grid, dim3(256), 0, st, a);  // also stores dS
   hipLaunchKernelGGL((mha_bwd_dq_kernel<DH>), grid, dim3(256), 0, st, a);
-  hipLaunchKernelGGL((mha_bwd_dkv_kernel<DH, 2>), grid, dim3(256), 0, st, a);
 }
 
 }  // namespace
@@ -584,7 +570,9 @@ int aur_mha_fwd(aur_ctx* ctx, const float* q, const float* k, const float* v, fl
 }
 
 size_t aur_mha_bwd_ws_bytes(uint32_t b, uint32_t t, uint32_t n_head) {
-  return (size_t)b * t * n_head * sizeof(float);
+  const size_t nqt = (t + TQ - 1) / TQ;
+  return ws_d_floats(b, t, n_head) * sizeof(float) +
+         (size_t)b * n_head * (nqt * (nqt + 1) / 2) * TQ * TQ * sizeof(float);
 }
 
 int aur_mha_bwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v, uint32_t ld_qkv,
@@ -603,6 +591,8 @@ int aur_mha_bwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v,
   AttnArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = out; a.dO = d_out; a.lse = const_cast<float*>(lse);
   a.D = ws; a.dq = dq; a.dk = dk; a.dv = dv;
+  a.ds = ws + ws_d_floats(b, t, n_head);
+  a.ntri = (int)(((t + TQ - 1) / TQ) * ((t + TQ - 1) / TQ + 1) / 2);
   a.ld_qkv = (int)ld_qkv; a.ld_o = (int)ld_out; a.ld_d = (int)ld_dqkv;
   a.T = (int)t; a.H = (int)n_head;
   a.scale = 1.0f / sqrtf((float)d_head);

@@ -145,8 +145,10 @@ DecoderTransformerGpu::DecoderTransformerGpu(aur_ctx* ctx, const TransformerConf
   const size_t per_layer = M * d /*ln1*/ + 2 * M /*stats*/ + 3 * M * d /*qkv*/ + M * d /*attn*/ +
                            H * M /*lse*/ + M * d /*xmid*/ + M * d /*ln2*/ + 2 * M + 2 * M * F;
   const size_t lnws = aur::layer_norm_backward_ws_floats((int)M, (int)d);
+  // attention backward: rowdot + the causal dS tiles of max_batch sequences
+  const size_t attn_ws_floats = (aur_mha_bwd_ws_bytes(max_batch, (uint32_t)Tm, (uint32_t)H) + 3) / 4;
   const size_t floats = L * per_layer + (L + 1) * M * d + M * d + 2 * M + M * V + M +
-                        4 * M * d + M * F + 3 * M * d + lnws + H * M + aur::grad_norm_ws_floats() + 16 +
+                        4 * M * d + M * F + 3 * M * d + lnws + attn_ws_floats + aur::grad_norm_ws_floats() + 16 +
                         (size_t)max_batch * d;
   const size_t ints = 3 * M + 2 * M + 2;
   const size_t bytes = floats * 4 + ints * 4 + 64 * 256 + 4096 * (L + 8);
@@ -181,7 +183,7 @@ DecoderTransformerGpu::DecoderTransformerGpu(aur_ctx* ctx, const TransformerConf
   A.dh = cv.take<float>(M * F);
   A.dqkv = cv.take<float>(3 * M * d);
   A.ln_ws = cv.take<float>(lnws);
-  A.attn_ws = cv.take<float>(H * M);
+  A.attn_ws = cv.take<float>(attn_ws_floats);
   A.norm_part = cv.take<float>(aur::grad_norm_ws_floats());
   A.stats = cv.take<float>(16);
   A.last = cv.take<float>((size_t)max_batch * d);

@@ -124,10 +124,12 @@ int aur_mha_fwd(aur_ctx* ctx, const float* q, const float* k, const float* v,
 
 /* Backward: dq, dk, dv are ACCUMULATED (+=), the caller zeroes them first
  * (attention.rs:575-578).  Deterministic: every output element has exactly
- * one writer, three passes (row dot D = Σ dO⊙O, dQ over key tiles, dK/dV
- * over query tiles).  `ws` is a caller-owned workspace of at least
- * aur_mha_bwd_ws_bytes(b, t, n_head) bytes (takes the slot of the reference's
- * d_scores_scratch [n_head,t,t]).
+ * one writer, three passes (row dot D = Σ dO⊙O; dK/dV over query tiles,
+ * which also stores the dS tiles of the causal lower triangle; dQ = dS·K
+ * over those tiles).  `ws` is a caller-owned workspace of at least
+ * aur_mha_bwd_ws_bytes(b, t, n_head) bytes: D [b,n_head,t] and the dS tiles,
+ * ≈ b·n_head·t²/2 floats (it takes the slot of the reference's
+ * d_scores_scratch [n_head,t,t] per sequence).
  * Replaces CausalMhaBackwardKernel::dispatch_into(ctx, enc, q, k, v, probs,
  * d_out, dq, dk, dv, d_scores_scratch, t, n_head, d_head)
  * (src/gpu/attention.rs:580-685). */

@@ -55,5 +55,7 @@ def test_workspace_size_helpers():
     from aurora_amd import _lib
 
     lib = _lib.load()
-    assert lib.aur_mha_bwd_ws_bytes(16, 1024, 8) == 16 * 1024 * 8 * 4
+    # D [b, H, t] (256-byte padded) + the 64×64 dS tiles of the causal lower triangle
+    assert lib.aur_mha_bwd_ws_bytes(16, 1024, 8) == (16 * 1024 * 8 + 16 * 8 * 136 * 4096) * 4
+    assert lib.aur_mha_bwd_ws_bytes(1, 65, 2) == (192 + 2 * 3 * 4096) * 4
     assert lib.aur_mha_kv_ws_bytes(32, 16, 768) >= 32 * 16 * 6 * 66 * 4
