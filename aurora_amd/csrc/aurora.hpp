@@ -276,9 +276,9 @@ class DecoderTransformerGpu {
   size_t n_params_ = 0, n_decay_ = 0;
   void* state_mem_ = nullptr;  // params | grads | m1 | m2
   void* muon_mem_ = nullptr;   // Muon momentum of the matrix region + Newton–Schulz scratch
-  float *mu_ = nullptr, *ns_upd_ = nullptr, *ns_x_[2] = {nullptr, nullptr}, *ns_bx_ = nullptr;
+  // per shape group: ns_x_ / ns_bx_ hold [matrices][m × nn], ns_a_ / ns_a2_ / ns_b_ [matrices][m × m]
+  float *mu_ = nullptr, *ns_x_[2] = {nullptr, nullptr}, *ns_bx_ = nullptr;
   float *ns_a_ = nullptr, *ns_a2_ = nullptr, *ns_b_ = nullptr, *muon_stats_ = nullptr;
-  void muon_matrix(float* p, const float* g, float* mu, uint32_t rows, uint32_t cols, const MuonConfig& c);
   void* act_mem_ = nullptr;
   float *params_ = nullptr, *grads_ = nullptr, *m1_ = nullptr, *m2_ = nullptr;
   std::vector<Layer>* layers_ = nullptr;

@@ -60,6 +60,11 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
          const Workspace* ws = nullptr);
 int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, const float* B,
          int ldb, float* C, int ldc, int M, int N, int K, bool accumulate);
+// `batch` independent C = op(A)·op(B) (store), problem z at A + z·sA,
+// B + z·sB, C + z·sC (strides in floats); one launch, no split-K.
+int gemm_batched(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, long long sA,
+                 const float* B, int ldb, long long sB, float* C, int ldc, long long sC, int M, int N, int K,
+                 int batch);
 // Decode-shaped A@Bᵀ (M ≤ 64) split into `splits` K ranges (each a multiple
 // of 64 long, none empty) whose products are stored to P[splits][M][N] for
 // the consumer to sum in range order.  gemm_nt_partials_splits gives the

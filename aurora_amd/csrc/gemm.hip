@@ -40,7 +40,19 @@ struct GemmArgs {
   int split;    // 1: write partial tiles to P[z] (epilogue runs in splitk_reduce)
   int tiles_m, tiles_n;
   aur::Epilogue epi;
+  // Strided batch (gridDim.y > 1): problem z uses A + z·sA, B + z·sB, C + z·sC.
+  long long sA, sB, sC;
 };
+
+// Points the operands at problem blockIdx.y of a strided batch.
+__device__ __forceinline__ void select_batch(GemmArgs& g) {
+  if (gridDim.y > 1) {
+    const long long z = blockIdx.y;
+    g.A += z * g.sA;
+    g.B += z * g.sB;
+    g.C += z * g.sC;
+  }
+}
 
 // Fused epilogue on one output element v = (A·B)(row, col), stored at C[i]
 // with i = row*ldc + col (R, X, C2 share C's layout).
@@ -212,6 +224,7 @@ __device__ __forceinline__ floatx4 read_frag(const float* __restrict__ s, int ro
 
 template <int BM, int BN, int BK, bool AK, bool BKC, bool VEC>
 __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
+  select_batch(g);
   using S = Smem<BM, BN, BK, AK, BKC>;
   constexpr int WM = BM / 2, WN = BN / 2;  // wave tile
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -354,6 +367,7 @@ struct DirectTile {
 
 template <int BM, int BN, bool AK, bool BKC>
 __global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
+  select_batch(g);
   using TA = DirectTile<BM, AK>;
   using TB = DirectTile<BN, BKC>;
   constexpr int ST = TA::ELEMS + TB::ELEMS;
@@ -707,7 +721,7 @@ constexpr int kBK = 32;
 // efficiency on MI355X (128×128: 1.00, 128×64: 0.90, 64×64: 0.88) times a
 // 0.97 penalty for the split-K reduction; splits keep ≥ 512 of K per block.
 // The highest score wins, ties going to the larger tile and fewer splits.
-Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split) {
+Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int batch = 1) {
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   struct Cand {
     int bm, bn, occ;
@@ -717,7 +731,7 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split) {
   Plan p{128, 128, 1, K};
   double best = -1.0;
   for (const Cand& c : cands) {
-    const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
     const long slots = (long)cus * c.occ;
     for (int s = 1; s <= 16; s *= 2) {
       if (s > 1 && (!allow_split || K / s < 512)) break;
@@ -751,8 +765,8 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split) {
 }
 
 template <int BM, int BN, bool AK, bool BKC>
-void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st) {
-  dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
+void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int batch) {
+  dim3 grid(a.tiles_m * a.tiles_n, batch, splits);
   const bool whole = vec && a.M % BM == 0 && a.N % BN == 0 && a.K % 32 == 0 && a.k_chunk % 32 == 0;
   if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr)
     hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC>), grid, dim3(kThreads), 0, st, a);
@@ -763,13 +777,13 @@ void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st) {
 }
 
 template <bool AK, bool BKC>
-void launch_layout(const GemmArgs& a, const Plan& p, bool vec, hipStream_t st) {
+void launch_layout(const GemmArgs& a, const Plan& p, bool vec, hipStream_t st, int batch = 1) {
   if (p.bm == 128 && p.bn == 128)
-    launch_tile<128, 128, AK, BKC>(a, p.splits, vec, st);
+    launch_tile<128, 128, AK, BKC>(a, p.splits, vec, st, batch);
   else if (p.bm == 128 && p.bn == 64)
-    launch_tile<128, 64, AK, BKC>(a, p.splits, vec, st);
+    launch_tile<128, 64, AK, BKC>(a, p.splits, vec, st, batch);
   else
-    launch_tile<64, 64, AK, BKC>(a, p.splits, vec, st);
+    launch_tile<64, 64, AK, BKC>(a, p.splits, vec, st, batch);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -930,6 +944,36 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
   Epilogue e;
   e.mode = accumulate ? EPI_ACCUM : EPI_STORE;
   return gemm(ctx, a_kcontig, b_kcontig, A, lda, B, ldb, C, ldc, M, N, K, e, nullptr);
+}
+
+int gemm_batched(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, long long sA,
+                 const float* B, int ldb, long long sB, float* C, int ldc, long long sC, int M, int N, int K,
+                 int batch) {
+  if (M < 1 || N < 1 || K < 1 || batch < 1 || batch > 65535)
+    return set_error(ctx, AUR_EINVAL, "gemm_batched: bad dims (M=%d N=%d K=%d batch=%d)", M, N, K, batch);
+  if (!A || !B || !C) return set_error(ctx, AUR_EINVAL, "gemm_batched: null pointer");
+  if (batch == 1) return gemm(ctx, a_kcontig, b_kcontig, A, lda, B, ldb, C, ldc, M, N, K, false);
+  const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) && (sA % 4 == 0) &&
+                   (sB % 4 == 0) && (a_kcontig ? (K % 4 == 0) : (M % 4 == 0)) &&
+                   (b_kcontig ? (K % 4 == 0) : (N % 4 == 0));
+  const Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/false, batch);
+  GemmArgs a{};
+  a.A = A; a.B = B; a.C = C; a.M = M; a.N = N; a.K = K;
+  a.lda = lda; a.ldb = ldb; a.ldc = ldc;
+  a.tiles_m = (M + p.bm - 1) / p.bm;
+  a.tiles_n = (N + p.bn - 1) / p.bn;
+  a.k_chunk = p.k_chunk;
+  a.sA = sA; a.sB = sB; a.sC = sC;
+  if (a_kcontig && b_kcontig)
+    launch_layout<true, true>(a, p, vec, ctx->stream, batch);
+  else if (a_kcontig && !b_kcontig)
+    launch_layout<true, false>(a, p, vec, ctx->stream, batch);
+  else if (!a_kcontig && b_kcontig)
+    launch_layout<false, true>(a, p, vec, ctx->stream, batch);
+  else
+    launch_layout<false, false>(a, p, vec, ctx->stream, batch);
+  AUR_LAUNCH_CHECK(ctx, "gemm_f32_mfma (batched)");
+  return 0;
 }
 
 int gemm_nt_partials_splits(int M, int N, int K) {

@@ -449,61 +449,45 @@ float DecoderTransformerGpu::clip_grads_adamw_subset(float max_norm) {
   return nrm;
 }
 
-void DecoderTransformerGpu::muon_matrix(float* p, const float* g, float* mu, uint32_t rows, uint32_t cols,
-                                        const MuonConfig& c) {
-  const size_t n = (size_t)rows * cols;
-  const int m = (int)std::min(rows, cols), nn = (int)std::max(rows, cols);
-  const bool transposed = rows > cols;
-  auto& A = *acts_;
-  aur::Epilogue store;
-  ck(ctx_, aur::muon_momentum(ctx_, g, mu, ns_upd_, n, c.momentum, c.nesterov), "muon momentum");
-  ck(ctx_, aur::frob_inv(ctx_, ns_upd_, n, A.norm_part, muon_stats_), "muon frobenius");
-  ck(ctx_, aur::scale_by(ctx_, ns_upd_, n, muon_stats_ + 1), "muon frobenius scale");
-  // X: the update in wide orientation [m × nn] (optimizer.rs:180-191).
-  float* x = ns_upd_;
-  int cur = 0;
-  if (transposed) {
-    ck(ctx_, aur::transpose(ctx_, ns_upd_, ns_x_[0], (int)rows, (int)cols), "muon load");
-    x = ns_x_[0];
-    cur = 0;
-  }
-  const float a_coef = 3.4445f, b_coef = -4.7750f, c_coef = 2.0315f;
-  for (uint32_t it = 0; it < c.ns_steps; ++it) {
-    float* nxt = (x == ns_x_[0]) ? ns_x_[1] : ns_x_[0];
-    // A = X·Xᵀ, A² = A·A, B = b·A + c·A², X' = a·X + B·X  (optimizer.rs:197-239)
-    ck(ctx_, aur::gemm(ctx_, true, true, x, nn, x, nn, ns_a_, m, m, m, nn, store), "ns xxt");
-    ck(ctx_, aur::gemm(ctx_, true, false, ns_a_, m, ns_a_, m, ns_a2_, m, m, m, m, store), "ns aa");
-    ck(ctx_, aur::axpby(ctx_, ns_b_, b_coef, ns_a_, c_coef, ns_a2_, (size_t)m * m), "ns combine");
-    ck(ctx_, aur::gemm(ctx_, true, false, ns_b_, m, x, nn, ns_bx_, nn, m, nn, m, store), "ns bx");
-    ck(ctx_, aur::axpby(ctx_, nxt, a_coef, x, 1.0f, ns_bx_, (size_t)m * nn), "ns step");
-    x = nxt;
-  }
-  (void)cur;
-  const float* upd = x;
-  if (transposed) {
-    ck(ctx_, aur::transpose(ctx_, x, ns_upd_, m, nn), "muon store");
-    upd = ns_upd_;
-  }
-  const float scale = std::sqrt((float)nn / (float)m);
-  ck(ctx_, aur::muon_apply(ctx_, p, upd, n, c.lr * scale, c.lr * c.weight_decay), "muon apply");
-}
-
+// Muon on every GEMM weight (optimizer.rs:115-305, gpu/transformer.rs:2100-2290),
+// batched by matrix shape: the per-matrix work (momentum, Frobenius bound,
+// orientation, update) is elementwise, and the 5 Newton–Schulz iterations of
+// all matrices of one wide shape m × nn run as strided-batched GEMMs — one
+// launch per product for the 4·L square matrices and one for the 2·L FFN
+// matrices, instead of 3 small GEMMs per matrix per iteration.  Each matrix's
+// arithmetic is the same as one at a time.
 void DecoderTransformerGpu::step_muon_hybrid(const MuonConfig& mc, const AdamWConfig& ac) {
-  const size_t d = cfg_.d_model, F = cfg_.d_ff, n_tok = (size_t)cfg_.vocab * d;
+  const size_t d = cfg_.d_model, F = cfg_.d_ff, L = cfg_.n_layer, n_tok = (size_t)cfg_.vocab * d;
+  struct Mat {
+    float* p;
+    uint32_t rows, cols;
+  };
+  // Matrices in the reference's order (gpu/transformer.rs:836-866), rows ×
+  // cols as it passes them (w_fc as d × d_ff, w_proj as d_ff × d), grouped by
+  // wide shape: square d × d (Q, K, V, O), then min(d,F) × max(d,F) (fc, proj).
+  std::vector<Mat> sq, ff;
+  for (uint32_t l = 0; l < L; ++l) {
+    Layer& Y = (*layers_)[l];
+    for (int i = 0; i < 3; ++i) sq.push_back({Y.w_qkv + i * d * d, (uint32_t)d, (uint32_t)d});
+    sq.push_back({Y.w_o, (uint32_t)d, (uint32_t)d});
+    ff.push_back({Y.w_fc, (uint32_t)d, (uint32_t)F});
+    ff.push_back({Y.w_proj, (uint32_t)F, (uint32_t)d});
+  }
+  const size_t m_ff = std::min(d, F), n_ff = std::max(d, F);
   if (!muon_mem_) {
     const size_t n_mat = n_decay_ - n_tok;
-    const size_t big = d * std::max(d, F), sq = d * d;
-    const size_t floats = n_mat + 4 * big + 3 * sq + 64;
+    const size_t xs = std::max(sq.size() * d * d, ff.size() * m_ff * n_ff);
+    const size_t as = std::max(sq.size() * d * d, ff.size() * m_ff * m_ff);
+    const size_t floats = n_mat + 3 * xs + 3 * as + 64;
     ck(ctx_, aur_malloc(ctx_, floats * sizeof(float) + 8 * 256, &muon_mem_), "alloc muon state");
     Carver cv{static_cast<char*>(muon_mem_)};
     mu_ = cv.take<float>(n_mat);
-    ns_upd_ = cv.take<float>(big);
-    ns_x_[0] = cv.take<float>(big);
-    ns_x_[1] = cv.take<float>(big);
-    ns_bx_ = cv.take<float>(big);
-    ns_a_ = cv.take<float>(sq);
-    ns_a2_ = cv.take<float>(sq);
-    ns_b_ = cv.take<float>(sq);
+    ns_x_[0] = cv.take<float>(xs);
+    ns_x_[1] = cv.take<float>(xs);
+    ns_bx_ = cv.take<float>(xs);
+    ns_a_ = cv.take<float>(as);
+    ns_a2_ = cv.take<float>(as);
+    ns_b_ = cv.take<float>(as);
     muon_stats_ = cv.take<float>(64);
     ck(ctx_, aur_memset0(ctx_, mu_, n_mat * sizeof(float)), "zero muon momentum");
   }
@@ -519,20 +503,56 @@ void DecoderTransformerGpu::step_muon_hybrid(const MuonConfig& mc, const AdamWCo
                       n_params_ - n_decay_, 0, nullptr, ac.lr, ac.beta1, ac.beta2, ac.eps, ac.weight_decay,
                       bc1, bc2),
      "adamw undecayed");
-  // Muon matrices, in the reference's order (gpu/transformer.rs:836-866):
-  // rows × cols as it passes them (w_fc as d × d_ff, w_proj as d_ff × d).
-  for (uint32_t l = 0; l < cfg_.n_layer; ++l) {
-    Layer& Y = (*layers_)[l];
-    auto go = [&](float* p, uint32_t rows, uint32_t cols) {
-      const size_t off = (size_t)(p - params_);
-      muon_matrix(p, grads_ + off, mu_ + (off - n_tok), rows, cols, mc);
-    };
-    go(Y.w_qkv, (uint32_t)d, (uint32_t)d);
-    go(Y.w_qkv + d * d, (uint32_t)d, (uint32_t)d);
-    go(Y.w_qkv + 2 * d * d, (uint32_t)d, (uint32_t)d);
-    go(Y.w_o, (uint32_t)d, (uint32_t)d);
-    go(Y.w_fc, (uint32_t)d, (uint32_t)F);
-    go(Y.w_proj, (uint32_t)F, (uint32_t)d);
+  auto& A = *acts_;
+  const float a_coef = 3.4445f, b_coef = -4.7750f, c_coef = 2.0315f;
+  for (const std::vector<Mat>* grp : {&sq, &ff}) {
+    const int nb = (int)grp->size();
+    const size_t m = grp == &sq ? d : m_ff, nn = grp == &sq ? d : n_ff, n = m * nn;
+    // X0[i] = the momentum update of matrix i, Frobenius-bounded, in wide
+    // orientation (optimizer.rs:143-191); ns_bx_ holds a tall one before its
+    // transpose.
+    for (int i = 0; i < nb; ++i) {
+      const Mat& M = (*grp)[i];
+      const size_t off = (size_t)(M.p - params_);
+      const bool tall = M.rows > M.cols;
+      float* u = (tall ? ns_bx_ : ns_x_[0]) + i * n;
+      ck(ctx_, aur::muon_momentum(ctx_, grads_ + off, mu_ + (off - n_tok), u, n, mc.momentum, mc.nesterov),
+         "muon momentum");
+      ck(ctx_, aur::frob_inv(ctx_, u, n, A.norm_part, muon_stats_), "muon frobenius");
+      ck(ctx_, aur::scale_by(ctx_, u, n, muon_stats_ + 1), "muon frobenius scale");
+      if (tall) ck(ctx_, aur::transpose(ctx_, u, ns_x_[0] + i * n, (int)M.rows, (int)M.cols), "muon load");
+    }
+    // Newton–Schulz quintic (optimizer.rs:197-239) on the whole group:
+    // A = X·Xᵀ, A² = A·A, B = b·A + c·A², X' = a·X + B·X.
+    float* x = ns_x_[0];
+    const int mi = (int)m, ni = (int)nn;
+    for (uint32_t it = 0; it < mc.ns_steps; ++it) {
+      float* nxt = (x == ns_x_[0]) ? ns_x_[1] : ns_x_[0];
+      ck(ctx_, aur::gemm_batched(ctx_, true, true, x, ni, (long long)n, x, ni, (long long)n, ns_a_, mi,
+                                 (long long)(m * m), mi, mi, ni, nb),
+         "ns xxt");
+      ck(ctx_, aur::gemm_batched(ctx_, true, false, ns_a_, mi, (long long)(m * m), ns_a_, mi, (long long)(m * m),
+                                 ns_a2_, mi, (long long)(m * m), mi, mi, mi, nb),
+         "ns aa");
+      ck(ctx_, aur::axpby(ctx_, ns_b_, b_coef, ns_a_, c_coef, ns_a2_, (size_t)nb * m * m), "ns combine");
+      ck(ctx_, aur::gemm_batched(ctx_, true, false, ns_b_, mi, (long long)(m * m), x, ni, (long long)n, ns_bx_,
+                                 ni, (long long)n, mi, ni, mi, nb),
+         "ns bx");
+      ck(ctx_, aur::axpby(ctx_, nxt, a_coef, x, 1.0f, ns_bx_, (size_t)nb * n), "ns step");
+      x = nxt;
+    }
+    // p ← p·(1 − lr·wd) − lr·√(max/min)·update, back in the matrix's own
+    // orientation (optimizer.rs:241-305).
+    const float scale = std::sqrt((float)nn / (float)m);
+    for (int i = 0; i < nb; ++i) {
+      const Mat& M = (*grp)[i];
+      const float* upd = x + i * n;
+      if (M.rows > M.cols) {
+        ck(ctx_, aur::transpose(ctx_, upd, ns_bx_ + i * n, mi, ni), "muon store");
+        upd = ns_bx_ + i * n;
+      }
+      ck(ctx_, aur::muon_apply(ctx_, M.p, upd, n, mc.lr * scale, mc.lr * mc.weight_decay), "muon apply");
+    }
   }
 }
 
