@@ -56,18 +56,33 @@ __device__ __forceinline__ void select_batch(GemmArgs& g) {
 
 // Fused epilogue on one output element v = (A·B)(row, col), stored at C[i]
 // with i = row*ldc + col (R, X, C2 share C's layout).
+// GELU, tanh form (src/linalg.rs:72-87): gelu(x) = 0.5·x·(1 + tanh(u)),
+// u = √(2/π)·(x + 0.044715·x³).  With σ(t) = 1/(1 + e^(−t)) the identities
+// 1 + tanh(u) = 2σ(2u) and sech²(u) = 4σ(2u)(1 − σ(2u)) give both the value
+// and the derivative from one exp2 and one reciprocal, with no cancellation:
+//   gelu(x)  = x·σ(2u)
+//   gelu'(x) = σ(2u) + 2x·σ(2u)(1 − σ(2u))·√(2/π)·(1 + 3·0.044715·x²)
+// (1 − σ(2u) = e^(−2u)·σ(2u) where σ is near 1).  The tanhf form spends
+// most of the FFN GEMM epilogues in VALU work.
+__device__ __forceinline__ float gelu_sigma(float x, float& one_minus) {
+  const float k = 0.7978845608028654f, log2e = 1.4426950408889634f;
+  const float u = k * (x + 0.044715f * x * x * x);
+  const float e = __builtin_amdgcn_exp2f(-2.0f * log2e * u);  // e^(−2u)
+  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
+  one_minus = e < 1.0f ? e * sig : 1.0f - sig;
+  return sig;
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
-  // src/linalg.rs:72-77: 0.5·x·(1 + tanh(√(2/π)·(x + 0.044715·x³)))
-  const float k = 0.7978845608028654f;
-  return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+  float om;
+  return x * gelu_sigma(x, om);
 }
 
 __device__ __forceinline__ float gelu_tanh_grad(float x) {
-  // src/linalg.rs:81-87
   const float k = 0.7978845608028654f;
-  const float th = tanhf(k * (x + 0.044715f * x * x * x));
-  const float sech2 = 1.0f - th * th;
-  return 0.5f * (1.0f + th) + 0.5f * x * sech2 * (k * (1.0f + 3.0f * 0.044715f * x * x));
+  float om;
+  const float sig = gelu_sigma(x, om);
+  return sig + 2.0f * x * sig * om * (k * (1.0f + 3.0f * 0.044715f * x * x));
 }
 
 __device__ __forceinline__ void apply_epilogue(const aur::Epilogue& e, float* __restrict__ C, size_t i,
@@ -131,6 +146,40 @@ __device__ __forceinline__ void write_tiles(const GemmArgs& g, const floatx4 (&a
     case aur::EPI_GELU_BWD: write_tile<aur::EPI_GELU_BWD>(g, acc, r0, c0, g16, l16, full); break;
     default: write_tile<aur::EPI_STORE>(g, acc, r0, c0, g16, l16, full); break;
   }
+}
+
+// The epilogue operand (R or X, laid out like C) of a wave's TM×TN tiles,
+// in the accumulator layout: pre[i][j][e] = S[r0 + 16i + 4·g16 + e][c0 + 16j + l16].
+template <int TM, int TN>
+__device__ __forceinline__ void load_epi_operand(const GemmArgs& g, floatx4 (&pre)[TM][TN], int r0, int c0,
+                                                 int g16, int l16, int mode) {
+  const float* src = mode == aur::EPI_RESID ? g.epi.R : g.epi.X;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pre[i][j][e] = src[(size_t)(r0 + i * 16 + 4 * g16 + e) * g.ldc + c0 + j * 16 + l16];
+}
+
+// write_tile for whole tiles whose epilogue operand was prefetched.
+template <int MODE, int TM, int TN>
+__device__ __forceinline__ void write_tile_pre(const GemmArgs& g, const floatx4 (&acc)[TM][TN],
+                                               const floatx4 (&pre)[TM][TN], int r0, int c0, int g16,
+                                               int l16) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const size_t idx = (size_t)(r0 + i * 16 + 4 * g16 + e) * g.ldc + c0 + j * 16 + l16;
+        if constexpr (MODE == aur::EPI_RESID)
+          g.C[idx] = pre[i][j][e] + acc[i][j][e];
+        else
+          g.C[idx] = acc[i][j][e] * gelu_tanh_grad(pre[i][j][e]);
+      }
 }
 
 template <int BM, int BN, int BK, bool AK, bool BKC>
@@ -365,7 +414,11 @@ struct DirectTile {
   }
 };
 
-template <int BM, int BN, bool AK, bool BKC>
+// PRE (epilogue operand prefetch, whole output tiles without split-K): the
+// residual R (EPI_RESID) or the activation X (EPI_GELU_BWD) of this wave's
+// tile is loaded into registers with the last K step, so its HBM latency
+// hides under the final MFMAs instead of stalling the store.
+template <int BM, int BN, bool AK, bool BKC, int PRE = 0>
 __global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
   select_batch(g);
   using TA = DirectTile<BM, AK>;
@@ -393,6 +446,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 pre[PRE != 0 ? TM : 1][PRE != 0 ? TN : 1];
 
   if (nk > 0) {
     TA::issue(g.A, g.lda, m0, kbeg, smem, wave, lane);
@@ -409,6 +463,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
       TA::issue(g.A, g.lda, m0, k0, na, wave, lane);
       TB::issue(g.B, g.ldb, n0, k0, na + TA::ELEMS, wave, lane);
     }
+    if constexpr (PRE != 0)
+      if (kt == nk - 1) load_epi_operand(g, pre, m0 + wm * WM, n0 + wn * WN, g16, l16, PRE);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       floatx4 fa[TM], fb[TN];
@@ -427,7 +483,12 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
     __syncthreads();
   }
 
-  write_tiles(g, acc, m0 + wm * WM, n0 + wn * WN, g16, l16, /*full=*/true);
+  if constexpr (PRE != 0) {
+    if (nk == 0) load_epi_operand(g, pre, m0 + wm * WM, n0 + wn * WN, g16, l16, PRE);
+    write_tile_pre<PRE>(g, acc, pre, m0 + wm * WM, n0 + wn * WN, g16, l16);
+  } else {
+    write_tiles(g, acc, m0 + wm * WM, n0 + wn * WN, g16, l16, /*full=*/true);
+  }
 }
 
 // v(m,n) = Σ_{z=0..splits-1} P[z][m][n] summed in increasing z, then the
@@ -768,8 +829,21 @@ template <int BM, int BN, bool AK, bool BKC>
 void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int batch) {
   dim3 grid(a.tiles_m * a.tiles_n, batch, splits);
   const bool whole = vec && a.M % BM == 0 && a.N % BN == 0 && a.K % 32 == 0 && a.k_chunk % 32 == 0;
-  if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr)
+  if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr) {
+    if constexpr (BM == 128 && BN == 128) {
+      if (!a.split && a.epi.mode == aur::EPI_RESID) {
+        hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, aur::EPI_RESID>), grid, dim3(kThreads), 0,
+                           st, a);
+        return;
+      }
+      if (!a.split && a.epi.mode == aur::EPI_GELU_BWD) {
+        hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, aur::EPI_GELU_BWD>), grid, dim3(kThreads), 0,
+                           st, a);
+        return;
+      }
+    }
     hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC>), grid, dim3(kThreads), 0, st, a);
+  }
   else if (vec)
     hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, kBK, AK, BKC, true>), grid, dim3(kThreads), 0, st, a);
   else
