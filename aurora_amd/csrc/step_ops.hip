@@ -123,6 +123,50 @@ __global__ void __launch_bounds__(256) ln_fwd_kernel(const float* __restrict__ x
   }
 }
 
+// Row-resident forms for d = 256·NV (the model widths): one wave per row,
+// float4 traffic, the row read once into registers and reused for the
+// statistics and the output.
+template <int NV>
+__global__ void __launch_bounds__(256) ln_fwd_vec_kernel(const float* __restrict__ x,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ beta,
+                                                         float* __restrict__ y, float* __restrict__ mean,
+                                                         float* __restrict__ rstd, int rows, float eps) {
+  constexpr int D = 256 * NV;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const floatx4* xr = reinterpret_cast<const floatx4*>(x + (size_t)r * D);
+  floatx4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = xr[lane + 64 * i];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+  const float mu = wave_sum(s) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q += (v[i][e] - mu) * (v[i][e] - mu);
+  const float is = 1.0f / sqrtf(wave_sum(q) / (float)D + eps);
+  const floatx4* g4 = reinterpret_cast<const floatx4*>(gamma);
+  const floatx4* b4 = reinterpret_cast<const floatx4*>(beta);
+  floatx4* yr = reinterpret_cast<floatx4*>(y + (size_t)r * D);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const floatx4 gg = g4[lane + 64 * i], bb = b4[lane + 64 * i];
+    floatx4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (v[i][e] - mu) * is * gg[e] + bb[e];
+    yr[lane + 64 * i] = o;
+  }
+  if (lane == 0) {
+    if (mean) mean[r] = mu;
+    if (rstd) rstd[r] = is;
+  }
+}
+
 // The same for few rows (decode: one row per sequence): one 256-thread block
 // per row, float4 traffic, so a launch over 32 rows is not latency-bound.
 // Requires d % 4 == 0 and 16-byte aligned rows.
@@ -261,6 +305,51 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(const float* __restrict__ x
     float v = s * (g - inv_d * (sg + xh * sgx));
     if (dr) v += dr[c];
     dxr[c] = v;
+  }
+}
+
+// ln_bwd_kernel for d = 256·NV: x, dy, γ (and dres) read once as float4.
+template <int NV>
+__global__ void __launch_bounds__(256) ln_bwd_vec_kernel(const float* __restrict__ x,
+                                                         const float* __restrict__ mean,
+                                                         const float* __restrict__ rstd,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ dy,
+                                                         const float* __restrict__ dres,
+                                                         float* __restrict__ dx, int rows) {
+  constexpr int D = 256 * NV;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float mu = mean[r], s = rstd[r];
+  const floatx4* xr = reinterpret_cast<const floatx4*>(x + (size_t)r * D);
+  const floatx4* dyr = reinterpret_cast<const floatx4*>(dy + (size_t)r * D);
+  const floatx4* g4 = reinterpret_cast<const floatx4*>(gamma);
+  floatx4 g[NV], xh[NV];
+  float sg = 0.f, sgx = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const floatx4 xv = xr[lane + 64 * i], dv = dyr[lane + 64 * i], gv = g4[lane + 64 * i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      g[i][e] = dv[e] * gv[e];
+      xh[i][e] = (xv[e] - mu) * s;
+      sg += g[i][e];
+      sgx += g[i][e] * xh[i][e];
+    }
+  }
+  sg = wave_sum(sg);
+  sgx = wave_sum(sgx);
+  const float inv_d = 1.0f / (float)D;
+  floatx4* dxr = reinterpret_cast<floatx4*>(dx + (size_t)r * D);
+  const floatx4* dr = dres ? reinterpret_cast<const floatx4*>(dres + (size_t)r * D) : nullptr;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    floatx4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = s * (g[i][e] - inv_d * (sg + xh[i][e] * sgx));
+    if (dr) o += dr[lane + 64 * i];
+    dxr[lane + 64 * i] = o;
   }
 }
 
@@ -576,12 +665,20 @@ int layer_norm_forward(aur_ctx* ctx, const float* x, const float* gamma, const f
   const bool vec = d % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
                                    reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) &
                                   15) == 0;
+  const dim3 g4((rows + 3) / 4);
   if (rows < 1024 && vec)
     hipLaunchKernelGGL(ln_fwd_rowblock_kernel, dim3(rows), dim3(256), 0, ctx->stream, x, gamma, beta, y, mean,
                        rstd, d, eps);
+  else if (vec && d == 256)
+    hipLaunchKernelGGL(ln_fwd_vec_kernel<1>, g4, dim3(256), 0, ctx->stream, x, gamma, beta, y, mean, rstd, rows, eps);
+  else if (vec && d == 512)
+    hipLaunchKernelGGL(ln_fwd_vec_kernel<2>, g4, dim3(256), 0, ctx->stream, x, gamma, beta, y, mean, rstd, rows, eps);
+  else if (vec && d == 1024)
+    hipLaunchKernelGGL(ln_fwd_vec_kernel<4>, g4, dim3(256), 0, ctx->stream, x, gamma, beta, y, mean, rstd, rows, eps);
+  else if (vec && d == 2048)
+    hipLaunchKernelGGL(ln_fwd_vec_kernel<8>, g4, dim3(256), 0, ctx->stream, x, gamma, beta, y, mean, rstd, rows, eps);
   else
-    hipLaunchKernelGGL(ln_fwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, ctx->stream, x, gamma, beta, y,
-                       mean, rstd, rows, d, eps);
+    hipLaunchKernelGGL(ln_fwd_kernel, g4, dim3(256), 0, ctx->stream, x, gamma, beta, y, mean, rstd, rows, d, eps);
   LAUNCH_OK(ctx, "ln_fwd_kernel");
 }
 
@@ -601,8 +698,20 @@ size_t layer_norm_backward_ws_floats(int rows, int d) {
 int layer_norm_backward(aur_ctx* ctx, const float* x, const float* mean, const float* rstd,
                         const float* gamma, const float* dy, const float* dres, float* dx,
                         float* dgamma, float* dbeta, float* ws, int rows, int d) {
-  hipLaunchKernelGGL(ln_bwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, ctx->stream, x, mean, rstd, gamma,
-                     dy, dres, dx, rows, d);
+  const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma) |
+                     reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(dres) |
+                     reinterpret_cast<uintptr_t>(dx)) & 15) == 0;
+  const dim3 g4((rows + 3) / 4);
+  if (vec && d == 256)
+    hipLaunchKernelGGL(ln_bwd_vec_kernel<1>, g4, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, rows);
+  else if (vec && d == 512)
+    hipLaunchKernelGGL(ln_bwd_vec_kernel<2>, g4, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, rows);
+  else if (vec && d == 1024)
+    hipLaunchKernelGGL(ln_bwd_vec_kernel<4>, g4, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, rows);
+  else if (vec && d == 2048)
+    hipLaunchKernelGGL(ln_bwd_vec_kernel<8>, g4, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, rows);
+  else
+    hipLaunchKernelGGL(ln_bwd_kernel, g4, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, rows, d);
   const int nch = (rows + LN_CHUNK - 1) / LN_CHUNK;
   float* pg = ws;
   float* pb = ws + (size_t)nch * d;

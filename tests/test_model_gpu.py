@@ -78,6 +78,22 @@ def test_config0_train_step_matches_cpu(ctx):
     m.destroy()
 
 
+def test_train_step_wide_rows_matches_cpu(ctx):
+    """d_model 256 over B·T = 1024 rows: the row-resident float4 LayerNorm
+    forward / backward paths (d = 256·k, ≥ 1024 rows) against the oracle."""
+    cfg = OM.Config(vocab=128, d_model=256, n_layer=1, n_head=4, d_ff=512, seq_len_max=256)
+    P = OM.init_params(cfg, 5)
+    tok, tgt = _tokens(cfg, 4, 256, 5)
+    m = _gpu_model(ctx, cfg, 4, P)
+    m.zero_grad()
+    loss_gpu = m.train_step_batch(tok, tgt)
+    loss_cpu, G = OM.batch_grads(P, cfg, tok, tgt)
+    assert abs(loss_gpu - loss_cpu) < 5e-3 * 4, (loss_gpu, loss_cpu)
+    worst = _compare_tree(m.read_tensors(grad=True), G, 1e-3, "grad")
+    print(f"[d256] loss gpu {loss_gpu:.6f} cpu {loss_cpu:.6f} |grad err| <= {worst:.2e}")
+    m.destroy()
+
+
 def test_fused_clip_adamw_equals_separate(ctx):
     cfg = C0
     P = OM.init_params(cfg, 1)
