@@ -366,7 +366,7 @@ def main() -> int:
         "attention": attn,
         "train": train,
         "decode": decode,
-        "roofline": {"bound": "mfma", "kernel": "gemm_f32_mfma (tied head, NT 8192x8192x512)",
+        "roofline": {"bound": "mfma", "kernel": "gemm_f32_mfma_direct<128,128> (tied head, NT 8192x8192x512)",
                      "achieved": round(head_tf, 3), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(head_tf / PEAK_FP32_MFMA, 4), "traffic": round(HEAD_TRAFFIC_BYTES),
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
