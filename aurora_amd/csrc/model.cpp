@@ -523,7 +523,8 @@ void DecoderTransformerGpu::step_muon_hybrid(const MuonConfig& mc, const AdamWCo
       if (tall) ck(ctx_, aur::transpose(ctx_, u, ns_x_[0] + i * n, (int)M.rows, (int)M.cols), "muon load");
     }
     // Newton–Schulz quintic (optimizer.rs:197-239) on the whole group:
-    // A = X·Xᵀ, A² = A·A, B = b·A + c·A², X' = a·X + B·X.
+    // A = X·Xᵀ, A² = A·A, B = b·A + c·A², X' = a·X + B·X — computed as
+    // X' = (a·I + B)·X, one product with no separate pass over X.
     float* x = ns_x_[0];
     const int mi = (int)m, ni = (int)nn;
     for (uint32_t it = 0; it < mc.ns_steps; ++it) {
@@ -534,11 +535,10 @@ void DecoderTransformerGpu::step_muon_hybrid(const MuonConfig& mc, const AdamWCo
       ck(ctx_, aur::gemm_batched(ctx_, true, false, ns_a_, mi, (long long)(m * m), ns_a_, mi, (long long)(m * m),
                                  ns_a2_, mi, (long long)(m * m), mi, mi, mi, nb),
          "ns aa");
-      ck(ctx_, aur::axpby(ctx_, ns_b_, b_coef, ns_a_, c_coef, ns_a2_, (size_t)nb * m * m), "ns combine");
-      ck(ctx_, aur::gemm_batched(ctx_, true, false, ns_b_, mi, (long long)(m * m), x, ni, (long long)n, ns_bx_,
-                                 ni, (long long)n, mi, ni, mi, nb),
-         "ns bx");
-      ck(ctx_, aur::axpby(ctx_, nxt, a_coef, x, 1.0f, ns_bx_, (size_t)nb * n), "ns step");
+      ck(ctx_, aur::ns_combine(ctx_, ns_b_, ns_a_, ns_a2_, a_coef, b_coef, c_coef, mi, nb), "ns combine");
+      ck(ctx_, aur::gemm_batched(ctx_, true, false, ns_b_, mi, (long long)(m * m), x, ni, (long long)n, nxt, ni,
+                                 (long long)n, mi, ni, mi, nb),
+         "ns step");
       x = nxt;
     }
     // p ← p·(1 − lr·wd) − lr·√(max/min)·update, back in the matrix's own

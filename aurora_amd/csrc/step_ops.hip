@@ -532,6 +532,18 @@ __global__ void __launch_bounds__(256) axpby_kernel(float* __restrict__ out, flo
     out[i] = alpha * x[i] + beta * y[i];
 }
 
+// Newton–Schulz coefficient matrix of nb stacked m × m matrices:
+// out = a·I + b·A + c·A², so that one product out·X gives a·X + (b·A + c·A²)·X.
+__global__ void __launch_bounds__(256) ns_combine_kernel(float* __restrict__ out, const float* __restrict__ A,
+                                                         const float* __restrict__ A2, float a, float b,
+                                                         float c, size_t m, size_t n) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const size_t e = i % (m * m);
+    out[i] = b * A[i] + c * A2[i] + (e / m == e % m ? a : 0.f);
+  }
+}
+
 // dst[c][r] = src[r][c] for src [rows × cols], through 32×33 LDS tiles so
 // both sides are coalesced (src/gpu/muon.rs:204-271 load/store).
 __global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ src, float* __restrict__ dst,
@@ -761,6 +773,14 @@ int muon_momentum(aur_ctx* ctx, const float* g, float* m, float* upd, size_t n, 
   hipLaunchKernelGGL(muon_momentum_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, g, m, upd, n, beta,
                      nesterov ? 1 : 0);
   LAUNCH_OK(ctx, "muon_momentum_kernel");
+}
+
+int ns_combine(aur_ctx* ctx, float* out, const float* A, const float* A2, float a, float b, float c, int m,
+               int nb) {
+  const size_t n = (size_t)nb * m * m;
+  hipLaunchKernelGGL(ns_combine_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, out, A, A2, a, b, c,
+                     (size_t)m, n);
+  LAUNCH_OK(ctx, "ns_combine_kernel");
 }
 
 int axpby(aur_ctx* ctx, float* out, float alpha, const float* x, float beta, const float* y, size_t n) {
