@@ -269,8 +269,8 @@ def main() -> int:
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py: this build measures ONE GPU only (one-GPU boxes; "
-              "the multi-GPU sharding is a design in DESIGN.md)", file=sys.stderr)
+        print("bench.py: this build measures ONE GPU only (every box has one GPU; "
+              "sharding across GPUs is designed, not built)", file=sys.stderr)
         return 2
 
     from aurora_amd.gpu import GpuContext

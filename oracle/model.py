@@ -51,8 +51,10 @@ DECAY_KEYS = {"w_q", "w_k", "w_v", "w_o", "w_fc", "w_proj"}  # + w_tok (model.rs
 def init_params(cfg: Config, seed: int) -> dict:
     """BASELINE init: every weight N(0, 0.02) (nanoGPT), the residual-branch
     outputs W_o and W_proj additionally × 1/sqrt(2·n_layer); LN γ = 1, β = 0.
-    (The reference's own init differs; parity only needs both
-    sides to start from the same tensors.)  Drawn from numpy's PCG64 in a
+    (The reference's own init differs — Xavier-uniform Q/K/V/fc, src/attention.rs:171-188,
+    zero W_o, src/transformer/attention.rs:59, embeddings U(±0.02·√3),
+    src/transformer/embedding.rs:34-43 — parity only needs both sides to start
+    from the same tensors.)  Drawn from numpy's PCG64 in a
     fixed order: w_tok, w_pos, then per layer w_q, w_k, w_v, w_o, w_fc, w_proj."""
     rng = np.random.default_rng(seed)
     d, F, V, T = cfg.d_model, cfg.d_ff, cfg.vocab, cfg.seq_len_max
