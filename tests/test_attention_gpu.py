@@ -232,3 +232,38 @@ def test_kv_step_batched_one_block_per_head(ctx, dh, monkeypatch):
     monkeypatch.setenv("AUR_KV_CHUNKED", "1")
     chunked = run()
     assert fro_rel(got, chunked) < 1e-5
+
+
+def test_config2_probability_rows_sum_to_one_and_lse(ctx):
+    """Size-free invariants at the config-2 shape (B16 H8 T1024 dh64): with
+    V = 1 every output is Σ_j P_ij = 1 exactly up to rounding (rows of P sum
+    to one), and with K = 0 every score is 0, so row i attends uniformly over
+    its i + 1 keys: lse_i = ln(i + 1) and O = the running mean of V."""
+    B, T, H, dh = 16, 1024, 8, 64
+    n = B * T * H * dh
+    rng = np.random.default_rng(3)
+    q, k = _n(rng, n), _n(rng, n)
+    ones = np.ones(n, np.float32)
+    o, _ = _fwd(ctx, q, k, ones, B, T, H, dh)
+    assert np.max(np.abs(o - 1.0)) < 1e-5, np.max(np.abs(o - 1.0))
+    v = _n(rng, n)
+    o, lse = _fwd(ctx, q, np.zeros(n, np.float32), v, B, T, H, dh)
+    want_lse = np.log(np.arange(1, T + 1, dtype=np.float64))
+    assert np.max(np.abs(lse.reshape(B, H, T) - want_lse)) < 1e-4
+    v4 = v.reshape(B, T, H, dh).astype(np.float64)
+    running = np.cumsum(v4, axis=1) / np.arange(1, T + 1)[None, :, None, None]
+    assert fro_rel(o.reshape(B, T, H, dh), running) < 1e-5
+
+
+def test_config2_zero_output_gradient_gives_zero_gradients(ctx):
+    """dO = 0 ⇒ dQ = dK = dV = 0 (every backward term carries dO or dP = dO·Vᵀ),
+    and the accumulate contract leaves non-zero destinations unchanged."""
+    B, T, H, dh = 4, 1024, 8, 64
+    n = B * T * H * dh
+    rng = np.random.default_rng(4)
+    q, k, v = _n(rng, n), _n(rng, n), _n(rng, n)
+    o, lse = _fwd(ctx, q, k, v, B, T, H, dh)
+    init = [_n(rng, n) for _ in range(3)]
+    dq, dk, dv = _bwd(ctx, q, k, v, o, lse, np.zeros(n, np.float32), B, T, H, dh, init=init)
+    for got, want in zip((dq, dk, dv), init):
+        np.testing.assert_array_equal(got, want)
