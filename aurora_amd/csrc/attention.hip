@@ -51,6 +51,7 @@ struct AttnArgs {
   int ld_d;          // row stride of dq, dk, dv
   int T, H;
   float scale;       // 1/sqrt(d_head)
+  int overwrite;     // backward: store dq/dk/dv instead of accumulating into them
 };
 
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
@@ -416,8 +417,8 @@ __global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
       if (!G::live(16 * d + 4 * g)) continue;
       floatx4* pk = reinterpret_cast<floatx4*>(dkr + 16 * d + 4 * g);
       floatx4* pv = reinterpret_cast<floatx4*>(dvr + 16 * d + 4 * g);
-      *pk = *pk + acc_k[d] * a.scale;
-      *pv = *pv + acc_v[d];
+      *pk = a.overwrite ? acc_k[d] * a.scale : *pk + acc_k[d] * a.scale;
+      *pv = a.overwrite ? acc_v[d] : *pv + acc_v[d];
     }
   }
 }
@@ -496,7 +497,7 @@ __global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
     for (int d = 0; d < NC; ++d) {
       if (!G::live(16 * d + 4 * g)) continue;
       floatx4* p = reinterpret_cast<floatx4*>(dqr + 16 * d + 4 * g);
-      *p = *p + acc[d] * a.scale;
+      *p = a.overwrite ? acc[d] * a.scale : *p + acc[d] * a.scale;
     }
   }
 }
@@ -539,6 +540,41 @@ void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
 
 }  // namespace
 
+// overwrite = 0: dq/dk/dv += (the C ABI's contract); 1: dq/dk/dv = (callers
+// that would otherwise zero them first).
+static int mha_bwd_impl(aur_ctx* ctx, int overwrite, const float* q, const float* k, const float* v,
+                        uint32_t ld_qkv, const float* out, const float* d_out, uint32_t ld_out, const float* lse,
+                        float* dq, float* dk, float* dv, uint32_t ld_dqkv, float* ws, uint32_t b, uint32_t t,
+                        uint32_t n_head, uint32_t d_head) {
+  AUR_CHECK_CTX(ctx);
+  if (int rc = check_common(ctx, b, t, n_head, d_head, ld_qkv, ld_out)) return rc;
+  if (ld_dqkv < n_head * d_head || (ld_dqkv & 3))
+    return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: bad gradient row stride %u", ld_dqkv);
+  if (!q || !k || !v || !out || !d_out || !lse || !dq || !dk || !dv || !ws)
+    return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: null pointer");
+  if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(d_out) || !al16(dq) || !al16(dk) ||
+      !al16(dv) || !al16(ws))
+    return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: tensors must be 16-byte aligned");
+  AttnArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = out; a.dO = d_out; a.lse = const_cast<float*>(lse);
+  a.D = ws; a.dq = dq; a.dk = dk; a.dv = dv;
+  a.ds = ws + ws_d_floats(b, t, n_head);
+  a.overwrite = overwrite;
+  a.ntri = (int)(((t + TQ - 1) / TQ) * ((t + TQ - 1) / TQ + 1) / 2);
+  a.ld_qkv = (int)ld_qkv; a.ld_o = (int)ld_out; a.ld_d = (int)ld_dqkv;
+  a.T = (int)t; a.H = (int)n_head;
+  a.scale = 1.0f / sqrtf((float)d_head);
+  switch (d_head) {
+    case 8: launch_bwd<8>(a, (int)b, ctx->stream); break;
+    case 16: launch_bwd<16>(a, (int)b, ctx->stream); break;
+    case 32: launch_bwd<32>(a, (int)b, ctx->stream); break;
+    default: launch_bwd<64>(a, (int)b, ctx->stream); break;
+  }
+  AUR_LAUNCH_CHECK(ctx, "mha_bwd kernels");
+  return 0;
+}
+
+
 extern "C" {
 
 int aur_mha_fwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v, uint32_t ld_qkv,
@@ -579,31 +615,8 @@ int aur_mha_bwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v,
                    const float* out, const float* d_out, uint32_t ld_out, const float* lse, float* dq,
                    float* dk, float* dv, uint32_t ld_dqkv, float* ws, uint32_t b, uint32_t t,
                    uint32_t n_head, uint32_t d_head) {
-  AUR_CHECK_CTX(ctx);
-  if (int rc = check_common(ctx, b, t, n_head, d_head, ld_qkv, ld_out)) return rc;
-  if (ld_dqkv < n_head * d_head || (ld_dqkv & 3))
-    return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: bad gradient row stride %u", ld_dqkv);
-  if (!q || !k || !v || !out || !d_out || !lse || !dq || !dk || !dv || !ws)
-    return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: null pointer");
-  if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(d_out) || !al16(dq) || !al16(dk) ||
-      !al16(dv) || !al16(ws))
-    return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: tensors must be 16-byte aligned");
-  AttnArgs a{};
-  a.q = q; a.k = k; a.v = v; a.o = out; a.dO = d_out; a.lse = const_cast<float*>(lse);
-  a.D = ws; a.dq = dq; a.dk = dk; a.dv = dv;
-  a.ds = ws + ws_d_floats(b, t, n_head);
-  a.ntri = (int)(((t + TQ - 1) / TQ) * ((t + TQ - 1) / TQ + 1) / 2);
-  a.ld_qkv = (int)ld_qkv; a.ld_o = (int)ld_out; a.ld_d = (int)ld_dqkv;
-  a.T = (int)t; a.H = (int)n_head;
-  a.scale = 1.0f / sqrtf((float)d_head);
-  switch (d_head) {
-    case 8: launch_bwd<8>(a, (int)b, ctx->stream); break;
-    case 16: launch_bwd<16>(a, (int)b, ctx->stream); break;
-    case 32: launch_bwd<32>(a, (int)b, ctx->stream); break;
-    default: launch_bwd<64>(a, (int)b, ctx->stream); break;
-  }
-  AUR_LAUNCH_CHECK(ctx, "mha_bwd kernels");
-  return 0;
+  return mha_bwd_impl(ctx, 0, q, k, v, ld_qkv, out, d_out, ld_out, lse, dq, dk, dv, ld_dqkv, ws, b, t, n_head,
+                      d_head);
 }
 
 int aur_mha_bwd(aur_ctx* ctx, const float* q, const float* k, const float* v, const float* out,
@@ -614,3 +627,15 @@ int aur_mha_bwd(aur_ctx* ctx, const float* q, const float* k, const float* v, co
 }
 
 }  // extern "C"
+
+namespace aur {
+
+int mha_bwd_store(aur_ctx* ctx, const float* q, const float* k, const float* v, int ld_qkv, const float* out,
+                  const float* d_out, int ld_out, const float* lse, float* dq, float* dk, float* dv, int ld_dqkv,
+                  float* ws, int b, int t, int n_head, int d_head) {
+  AUR_CHECK_CTX(ctx);
+  return mha_bwd_impl(ctx, 1, q, k, v, (uint32_t)ld_qkv, out, d_out, (uint32_t)ld_out, lse, dq, dk, dv,
+                      (uint32_t)ld_dqkv, ws, (uint32_t)b, (uint32_t)t, (uint32_t)n_head, (uint32_t)d_head);
+}
+
+}  // namespace aur

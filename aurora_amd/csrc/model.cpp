@@ -330,9 +330,9 @@ void DecoderTransformerGpu::encode_backward(uint32_t b, uint32_t t) {
     // MHA (transformer/attention.rs:221-334)
     ck(ctx_, aur::gemm(ctx_, true, false, dpa, d, Y.w_o, d, A.dattn, d, M, d, d, false), "w_o dX");
     ck(ctx_, aur::gemm(ctx_, false, false, dpa, d, Y.attn, d, Y.g_w_o, d, d, d, M, true), "w_o dW");
-    ck(ctx_, aur_memset0(ctx_, A.dqkv, (size_t)M * 3 * d * sizeof(float)), "zero dqkv");
-    ck(ctx_, aur_mha_bwd_ex(ctx_, Y.qkv, Y.qkv + d, Y.qkv + 2 * d, 3 * d, Y.attn, A.dattn, d, Y.lse, A.dqkv,
-                            A.dqkv + d, A.dqkv + 2 * d, 3 * d, A.attn_ws, b, t, H, dh),
+    // dq, dk, dv stored (not accumulated) into the fused [M, 3d] gradient
+    ck(ctx_, aur::mha_bwd_store(ctx_, Y.qkv, Y.qkv + d, Y.qkv + 2 * d, 3 * d, Y.attn, A.dattn, d, Y.lse, A.dqkv,
+                                A.dqkv + d, A.dqkv + 2 * d, 3 * d, A.attn_ws, (int)b, (int)t, H, dh),
        "mha_bwd");
     // dx_q + dx_k + dx_v = dqkv · [w_q; w_k; w_v];  g_w_qkv += dqkvᵀ · ln1
     ck(ctx_, aur::gemm(ctx_, true, false, A.dqkv, 3 * d, Y.w_qkv, d, A.dln, d, M, d, 3 * d, false), "qkv dX");

@@ -61,6 +61,11 @@ int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* ou
 int gather_rows(aur_ctx* ctx, const float* src, int ld_src, int row_step, int row_off, float* dst,
                 int rows, int d);
 
+// aur_mha_bwd_ex that STORES dq/dk/dv instead of accumulating (attention.hip).
+int mha_bwd_store(aur_ctx* ctx, const float* q, const float* k, const float* v, int ld_qkv, const float* out,
+                  const float* d_out, int ld_out, const float* lse, float* dq, float* dk, float* dv, int ld_dqkv,
+                  float* ws, int b, int t, int n_head, int d_head);
+
 // Batched KV decode attention with q rows of stride ld_q (kv_decode.hip).
 // k_new/v_new (same stride as q): the row at position t_total-1 is taken from
 // them and appended to the history by the kernel.
