@@ -53,7 +53,25 @@ struct KvArgs {
   // owns it writes it into the history.  Null: the history already has it.
   const float* knew;
   const float* vnew;
+  // q, knew and vnew may be K-range partial products of the QKV projection:
+  // the value is the sum of nparts (≤ 8) rows pstride floats apart, in order.
+  int nparts;
+  size_t pstride;
 };
+
+// Σ_z p[z·stride] for z < np (≤ 8), ascending; the loads are all issued
+// before the adds (clamped index, branch-free).
+__device__ __forceinline__ floatx4 sum_parts(const float* p, int np, size_t stride) {
+  if (np <= 1) return *reinterpret_cast<const floatx4*>(p);
+  floatx4 t[8];
+#pragma unroll
+  for (int z = 0; z < 8; ++z) t[z] = *reinterpret_cast<const floatx4*>(p + (size_t)min(z, np - 1) * stride);
+  floatx4 v = t[0];
+#pragma unroll
+  for (int z = 1; z < 8; ++z)
+    if (z < np) v += t[z];
+  return v;
+}
 
 // out[b, h*DH + d] = Σ_c 2^(m_c − M) o_c[d] / Σ_c 2^(m_c − M) l_c, c ascending.
 template <int DH>
@@ -88,7 +106,7 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
     if (tid < PART) rec[tid] = tid == 0 ? -INFINITY : 0.f;
   } else {
     const size_t hist = (size_t)b * a.max_len;
-    floatx4 qv = *reinterpret_cast<const floatx4*>(a.q + (size_t)b * a.ld_q + h * DH + 4 * part);
+    floatx4 qv = sum_parts(a.q + (size_t)b * a.ld_q + h * DH + 4 * part, a.nparts, a.pstride);
     qv *= a.scale * LOG2E;
 
     // Every K and V row of this wave's keys is requested before any math, so
@@ -101,8 +119,8 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
       if (key < T) {
         if (a.knew && key == T - 1) {
           const size_t o = (size_t)b * a.ld_q + h * DH + 4 * part;
-          kv = *reinterpret_cast<const floatx4*>(a.knew + o);
-          vv = *reinterpret_cast<const floatx4*>(a.vnew + o);
+          kv = sum_parts(a.knew + o, a.nparts, a.pstride);
+          vv = sum_parts(a.vnew + o, a.nparts, a.pstride);
           *reinterpret_cast<floatx4*>(const_cast<float*>(a.kh) + (hist + key) * a.ld + h * DH + 4 * part) = kv;
           *reinterpret_cast<floatx4*>(const_cast<float*>(a.vh) + (hist + key) * a.ld + h * DH + 4 * part) = vv;
         } else {
@@ -185,43 +203,64 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
   constexpr int ROUND = SW * U * KPS;
   __shared__ float wm[SW], wl[SW];
   __shared__ __attribute__((aligned(16))) float wo[SW][DH];
+  __shared__ __attribute__((aligned(16))) float qkn[3][DH];  // q (scaled), new k, new v of this head
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane / LPK, part = lane % LPK;
   const int h = blockIdx.x, b = blockIdx.y;
   const int T = min(a.t_dev ? a.t_dev[b] : a.t_scalar, t_max);
   const size_t hist = (size_t)b * a.max_len;
   const size_t col = (size_t)h * DH + 4 * part;
-  const float* krow_new = a.knew ? a.knew + (size_t)b * a.ld_q + col : nullptr;
-  const float* vrow_new = a.vnew ? a.vnew + (size_t)b * a.ld_q + col : nullptr;
-  // Fused append: the new row (position T-1) goes into the history; the
-  // attention below reads it from knew/vnew, so this store has no reader.
-  if (a.knew && T >= 1 && w == 0 && g == 0) {
-    *reinterpret_cast<floatx4*>(const_cast<float*>(a.kh) + (hist + T - 1) * a.ld + col) =
-        *reinterpret_cast<const floatx4*>(krow_new);
-    *reinterpret_cast<floatx4*>(const_cast<float*>(a.vh) + (hist + T - 1) * a.ld + col) =
-        *reinterpret_cast<const floatx4*>(vrow_new);
+  // One lane group reads q and the new K/V row (summing the QKV partials)
+  // and shares them through LDS; it also appends the new row (position
+  // T-1) to the history, which nothing in this launch reads back.
+  if (w == 0 && g == 0) {
+    const size_t o = (size_t)b * a.ld_q + col;
+    const floatx4 q4 = sum_parts(a.q + o, a.nparts, a.pstride) * (a.scale * LOG2E);
+    *reinterpret_cast<floatx4*>(&qkn[0][4 * part]) = q4;
+    if (a.knew) {
+      const floatx4 k4 = sum_parts(a.knew + o, a.nparts, a.pstride);
+      const floatx4 v4 = sum_parts(a.vnew + o, a.nparts, a.pstride);
+      *reinterpret_cast<floatx4*>(&qkn[1][4 * part]) = k4;
+      *reinterpret_cast<floatx4*>(&qkn[2][4 * part]) = v4;
+      if (T >= 1) {
+        *reinterpret_cast<floatx4*>(const_cast<float*>(a.kh) + (hist + T - 1) * a.ld + col) = k4;
+        *reinterpret_cast<floatx4*>(const_cast<float*>(a.vh) + (hist + T - 1) * a.ld + col) = v4;
+      }
+    }
   }
-  floatx4 qv = *reinterpret_cast<const floatx4*>(a.q + (size_t)b * a.ld_q + col);
-  qv *= a.scale * LOG2E;
   const int last = max(T - 1, 0);
+  // History rows only: the new row's slot may be mid-append (every value in
+  // it is finite either way); key T-1 takes the shared row before use.
   auto load = [&](int base, floatx4* kr, floatx4* vr) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int key = min(base + (u * SW + w) * KPS + g, last);
-      const bool is_new = a.knew != nullptr && key == T - 1;
-      const float* kp = is_new ? krow_new : a.kh + (hist + key) * a.ld + col;
-      const float* vp = is_new ? vrow_new : a.vh + (hist + key) * a.ld + col;
-      kr[u] = *reinterpret_cast<const floatx4*>(kp);
-      vr[u] = *reinterpret_cast<const floatx4*>(vp);
+      kr[u] = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + col);
+      vr[u] = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + col);
     }
   };
   float m = -INFINITY, l = 0.f;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
   floatx4 kc[U], vc[U];
   load(0, kc, vc);
+  __syncthreads();
+  const floatx4 qv = *reinterpret_cast<const floatx4*>(&qkn[0][4 * part]);
+  floatx4 knew_v = {0.f, 0.f, 0.f, 0.f}, vnew_v = {0.f, 0.f, 0.f, 0.f};
+  if (a.knew) {
+    knew_v = *reinterpret_cast<const floatx4*>(&qkn[1][4 * part]);
+    vnew_v = *reinterpret_cast<const floatx4*>(&qkn[2][4 * part]);
+  }
   for (int base = 0; base < T; base += ROUND) {
     floatx4 kn[U], vn[U];
     load(base + ROUND, kn, vn);  // clamped: past the end it re-reads the last row (cached)
+    if (a.knew) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (base + (u * SW + w) * KPS + g == T - 1) {
+          kc[u] = knew_v;
+          vc[u] = vnew_v;
+        }
+    }
     float sc[U];
     float mx = -INFINITY;
 #pragma unroll
@@ -365,7 +404,8 @@ namespace aur {
 
 int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_history,
                    const float* v_history, float* out, float* scratch, const int32_t* t_total, int t_max,
-                   int b, int n_head, int d_head, int max_len, const float* k_new, const float* v_new) {
+                   int b, int n_head, int d_head, int max_len, const float* k_new, const float* v_new,
+                   int nparts, size_t part_stride) {
   if (!dh_ok((uint32_t)d_head))
     return set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%d, supports 8/16/32/64", d_head);
   if (b <= 0 || n_head <= 0 || t_max <= 0 || t_max > max_len || ld_q < n_head * d_head || (ld_q & 3))
@@ -373,12 +413,15 @@ int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_histor
                      max_len, ld_q);
   if (!q || !k_history || !v_history || !out || !scratch || !t_total || (!k_new != !v_new))
     return set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: null pointer");
+  if (nparts < 1 || nparts > 8 || (nparts > 1 && (part_stride < (size_t)b * ld_q || (part_stride & 3))))
+    return set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: nparts=%d part_stride=%zu", nparts, part_stride);
   KvArgs a{};
   a.q = q; a.kh = k_history; a.vh = v_history; a.out = out; a.ws = scratch;
   a.t_dev = t_total; a.t_scalar = 0;
   a.ld = n_head * d_head; a.ld_q = ld_q; a.max_len = max_len; a.H = n_head;
   a.scale = 1.0f / sqrtf((float)d_head);
   a.knew = k_new; a.vnew = v_new;
+  a.nparts = nparts; a.pstride = part_stride;
   return launch(ctx, a, b, t_max, d_head);
 }
 

@@ -43,6 +43,17 @@ struct Carver {
 
 inline void ck(aur_ctx* ctx, int rc, const char* what) { check(ctx, rc, what); }
 
+// K ranges of the decode QKV projection (K = d_model): ranges of 128, at most
+// 8, tiling K the way gemm_nt_partials does (multiples of 64).
+int qkv_splits(size_t d) {
+  int s = (int)std::max<size_t>(1, std::min<size_t>(8, d / 128));
+  for (; s > 1; --s) {
+    const size_t chunk = ((d + s - 1) / s + 63) / 64 * 64;
+    if ((d + chunk - 1) / chunk == (size_t)s) break;
+  }
+  return s;
+}
+
 }  // namespace
 
 struct DecoderTransformerGpu::Layer {
@@ -592,8 +603,12 @@ KvCacheGpu::KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch_, uint
   part_floats_ = (size_t)std::max(aur::gemm_nt_partials_splits((int)B, (int)d, (int)d),
                                   aur::gemm_nt_partials_splits((int)B, (int)d, (int)F)) *
                  B * d;
-  // x, ln, qkv (3), attn, xmid = 7 rows of d per sequence
-  const size_t floats = 2 * hist + B * (d * 7 + 2 * F + V) + scratch + part_floats_;
+  // The decode QKV projection as qkv_parts K-range partials [parts][B][3d]
+  // that the attention kernel sums (B ≤ 64), else one product.
+  qkv_parts = batch <= 64 ? qkv_splits(d) : 1;
+  // x, ln, qkv (3 per part), attn, xmid rows of d per sequence
+  const size_t floats =
+      2 * hist + B * (d * (4 + 3 * (size_t)qkv_parts) + 2 * F + V) + scratch + part_floats_;
   bytes_ = floats * 4 + 3 * B * 4 + 32 * 256;
   ck(ctx_, aur_malloc(ctx_, bytes_, &mem_), "KvCacheGpu alloc");
   Carver cv{static_cast<char*>(mem_)};
@@ -601,7 +616,7 @@ KvCacheGpu::KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch_, uint
   v_ = cv.take<float>(hist);
   x_ = cv.take<float>(B * d);
   ln_ = cv.take<float>(B * d);
-  qkv_ = cv.take<float>(3 * B * d);
+  qkv_ = cv.take<float>((size_t)qkv_parts * 3 * B * d);
   attn_ = cv.take<float>(B * d);
   xmid_ = cv.take<float>(B * d);
   hpre_ = cv.take<float>(B * F);
@@ -728,12 +743,19 @@ void DecoderTransformerGpu::encode_decode_step(KvCacheGpu& cache) {
       ck(ctx_, aur::layer_norm_forward(ctx_, cache.x_, Y.ln1_g, Y.ln1_b, cache.ln_, nullptr, nullptr, B, d,
                                        kLnEps),
          "ln1");
-    ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, Y.w_qkv, d, cache.qkv_, 3 * d, B, 3 * d, d, store), "qkv");
+    // qkv as K-range partials that the attention kernel sums: short K ranges
+    // keep the X bytes each CU reads below its weight bytes
+    if (cache.qkv_parts > 1)
+      ck(ctx_, aur::gemm_nt_partials(ctx_, cache.ln_, d, Y.w_qkv, d, cache.qkv_, B, 3 * d, d, cache.qkv_parts),
+         "qkv");
+    else
+      ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, Y.w_qkv, d, cache.qkv_, 3 * d, B, 3 * d, d, store),
+         "qkv");
     // attention of the new query over history + the new row, which the
     // kernel also appends to the history (kv_cache.rs:169-179)
     ck(ctx_, aur::mha_kv_batched(ctx_, cache.qkv_, 3 * d, cache.k_history(l), cache.v_history(l), cache.attn_,
                                  cache.scratch_, cache.lens_, t_max, B, H, dh, (int)cache.max_len,
-                                 cache.qkv_ + d, cache.qkv_ + 2 * d),
+                                 cache.qkv_ + d, cache.qkv_ + 2 * d, cache.qkv_parts, (size_t)B * 3 * d),
        "mha_kv");
     if (split) {
       ck(ctx_, aur::gemm_nt_partials(ctx_, cache.attn_, d, Y.w_o, d, cache.part_, B, d, d, s_o), "w_o");

@@ -68,10 +68,12 @@ int mha_bwd_store(aur_ctx* ctx, const float* q, const float* k, const float* v, 
 
 // Batched KV decode attention with q rows of stride ld_q (kv_decode.hip).
 // k_new/v_new (same stride as q): the row at position t_total-1 is taken from
-// them and appended to the history by the kernel.
+// them and appended to the history by the kernel.  nparts > 1: q, k_new and
+// v_new are each the sum of nparts (≤ 8) K-range partial rows part_stride
+// floats apart (the QKV projection's partials), summed in order.
 int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_history,
                    const float* v_history, float* out, float* scratch, const int32_t* t_total, int t_max,
                    int b, int n_head, int d_head, int max_len, const float* k_new = nullptr,
-                   const float* v_new = nullptr);
+                   const float* v_new = nullptr, int nparts = 1, size_t part_stride = 0);
 
 }  // namespace aur
