@@ -522,18 +522,10 @@ __global__ void __launch_bounds__(256) muon_momentum_kernel(const float* __restr
   }
 }
 
-// out = α·x + β·y — the Newton–Schulz combines B = b·A + c·A² and
-// X' = a·X + B·X (src/gpu/muon.rs:421-515).
-__global__ void __launch_bounds__(256) axpby_kernel(float* __restrict__ out, float alpha,
-                                                    const float* __restrict__ x, float beta,
-                                                    const float* __restrict__ y, size_t n) {
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-    out[i] = alpha * x[i] + beta * y[i];
-}
-
 // Newton–Schulz coefficient matrix of nb stacked m × m matrices:
-// out = a·I + b·A + c·A², so that one product out·X gives a·X + (b·A + c·A²)·X.
+// out = a·I + b·A + c·A², so that one product out·X gives a·X + (b·A + c·A²)·X
+// (the reference combines B = b·A + c·A² and X' = a·X + B·X in two passes,
+// src/gpu/muon.rs:421-515).
 __global__ void __launch_bounds__(256) ns_combine_kernel(float* __restrict__ out, const float* __restrict__ A,
                                                          const float* __restrict__ A2, float a, float b,
                                                          float c, size_t m, size_t n) {
@@ -781,11 +773,6 @@ int ns_combine(aur_ctx* ctx, float* out, const float* A, const float* A2, float 
   hipLaunchKernelGGL(ns_combine_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, out, A, A2, a, b, c,
                      (size_t)m, n);
   LAUNCH_OK(ctx, "ns_combine_kernel");
-}
-
-int axpby(aur_ctx* ctx, float* out, float alpha, const float* x, float beta, const float* y, size_t n) {
-  hipLaunchKernelGGL(axpby_kernel, dim3(grid_1d(n)), dim3(256), 0, ctx->stream, out, alpha, x, beta, y, n);
-  LAUNCH_OK(ctx, "axpby_kernel");
 }
 
 int transpose(aur_ctx* ctx, const float* src, float* dst, int rows, int cols) {

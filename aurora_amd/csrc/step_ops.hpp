@@ -42,7 +42,6 @@ int grad_norm2(aur_ctx* ctx, const float* g1, size_t n1, const float* g2, size_t
 int frob_inv(aur_ctx* ctx, const float* x, size_t n, float* part, float* stats);
 // Muon pieces (optimizer.rs:147-305, gpu/muon.rs).
 int muon_momentum(aur_ctx* ctx, const float* g, float* m, float* upd, size_t n, float beta, bool nesterov);
-int axpby(aur_ctx* ctx, float* out, float alpha, const float* x, float beta, const float* y, size_t n);
 // out = a·I + b·A + c·A² for nb stacked m × m matrices (Newton–Schulz).
 int ns_combine(aur_ctx* ctx, float* out, const float* A, const float* A2, float a, float b, float c, int m,
                int nb);
