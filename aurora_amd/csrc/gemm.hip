@@ -808,8 +808,7 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int 
     }
   }
   // Tuning override: AUR_GEMM_CFG="BMxBN[:splits]".
-  static const char* const env = std::getenv("AUR_GEMM_CFG");  // read once per process
-  if (env) {
+  if (const char* env = std::getenv("AUR_GEMM_CFG")) {
     int bm = 0, bn = 0, sp = 1;
     if (std::sscanf(env, "%dx%d:%d", &bm, &bn, &sp) >= 2 &&
         ((bm == 128 && bn == 128) || (bm == 128 && bn == 64) || (bm == 64 && bn == 64))) {
@@ -830,8 +829,7 @@ template <int BM, int BN, bool AK, bool BKC>
 void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int batch) {
   dim3 grid(a.tiles_m * a.tiles_n, batch, splits);
   const bool whole = vec && a.M % BM == 0 && a.N % BN == 0 && a.K % 32 == 0 && a.k_chunk % 32 == 0;
-  static const bool staged_only = std::getenv("AUR_GEMM_STAGED") != nullptr;  // read once per process
-  if (whole && !staged_only) {
+  if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr) {
     if constexpr (BM == 128 && BN == 128) {
       if (!a.split && a.epi.mode == aur::EPI_RESID) {
         hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, aur::EPI_RESID>), grid, dim3(kThreads), 0,
@@ -926,8 +924,7 @@ static int skinny_nt(aur_ctx* ctx, const float* A, int lda, const float* B, int 
   while (u < 8 && w * u < nck) u *= 2;
   if (mt == 4 && u > 4) u = 4;
   if (mt < 4 && w == 16 && u > 4) u = 4;
-  static const char* const env = std::getenv("AUR_SKINNY_CFG");  // read once per process
-  if (env) {
+  if (const char* env = std::getenv("AUR_SKINNY_CFG")) {
     int ew = 0, eu = 0;
     if (std::sscanf(env, "%d:%d", &ew, &eu) == 2 && (ew == 4 || ew == 8 || ew == 16) &&
         (eu == 1 || eu == 2 || eu == 4 || eu == 8) && !(mt == 4 && (ew == 16 || eu == 8)) &&
