@@ -774,36 +774,47 @@ struct Plan {
 
 constexpr int kBK = 32;
 
-// Launch plan: tile shape and split-K count.  A CU holds two 128×128, three
-// 128×64 or five 64×64 blocks (LDS of the direct-load kernel), so a launch
-// runs in "waves" of CUs × occupancy blocks and a partly filled last wave idles the rest of
-// the chip.  Each candidate (tile, splits) is scored by its wave
-// quantisation efficiency times the tile's measured relative MFMA
-// efficiency on MI355X (128×128: 1.00, 128×64: 0.90, 64×64: 0.88) times a
-// 0.97 penalty for the split-K reduction; splits keep ≥ 512 of K per block.
-// The highest score wins, ties going to the larger tile and fewer splits.
-Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int batch = 1) {
+// Launch plan: tile shape and split-K count, chosen by a time model.  Blocks
+// are spread over the CUs, so the busiest CU runs L = ceil(blocks / CUs)
+// blocks of f = 2·BM·BN·k_chunk FLOP each, at the CU's peak (256 FLOP/clk)
+// times the tile's relative MFMA efficiency, and slower still when the CU
+// holds a single block (one wave per SIMD leaves LDS and barrier latency
+// exposed).  Split-K adds its reduction pass: the partial planes, the output
+// and any epilogue operand (extra_planes) through HBM, plus one launch.
+// Splits keep ≥ 512 of K per block.  The lowest modelled time wins, ties
+// going to the larger tile and fewer splits.  The constants were fitted on
+// MI355X to every forced configuration of 49 shapes (A@B, A@Bᵀ and the
+// weight-gradient accumulate at M = 1024…16384): tile efficiency 1.00 /
+// 0.95 / 0.85 (128×128 / 128×64 / 64×64), single-block factor 0.8 / 0.7 /
+// 0.7, 3 TB/s for the reduction and 2 µs per launch; the pick is within 1 %
+// of the measured best on all but one (a 1024×512×512 GEMM, 7 %).
+Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int batch = 1,
+                 int extra_planes = 0) {
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  constexpr double kCuFlops = 256.0 * 2.4e9;  // FLOP/s per CU, fp32 MFMA
+  constexpr double kHbm = 3.0e12, kLaunch = 2.0e-6;
   struct Cand {
-    int bm, bn, occ;
-    double eff;
+    int bm, bn;
+    double eff, single;
   };
-  static constexpr Cand cands[] = {{128, 128, 2, 1.00}, {128, 64, 3, 0.90}, {64, 64, 5, 0.88}};
+  static constexpr Cand cands[] = {{128, 128, 1.00, 0.8}, {128, 64, 0.95, 0.7}, {64, 64, 0.85, 0.7}};
   Plan p{128, 128, 1, K};
-  double best = -1.0;
+  double best = 1e30;
   for (const Cand& c : cands) {
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
-    const long slots = (long)cus * c.occ;
     for (int s = 1; s <= 16; s *= 2) {
       if (s > 1 && (!allow_split || K / s < 512)) break;
-      const long blocks = tiles * s;
-      const long waves = (blocks + slots - 1) / slots;
-      const double score = (double)blocks / (double)(waves * slots) * c.eff * (s > 1 ? 0.97 : 1.0);
-      if (score > best + 1e-9) {
-        best = score;
-        int chunk = (K + s - 1) / s;
-        chunk = (chunk + kBK - 1) / kBK * kBK;
-        p = {c.bm, c.bn, (K + chunk - 1) / chunk, chunk};
+      int chunk = (K + s - 1) / s;
+      chunk = (chunk + kBK - 1) / kBK * kBK;
+      const int splits = (K + chunk - 1) / chunk;
+      const long blocks = tiles * splits;
+      const long per_cu = (blocks + cus - 1) / cus;
+      const double f = 2.0 * c.bm * c.bn * chunk;
+      double t = per_cu * f / (kCuFlops * c.eff * (per_cu == 1 ? c.single : 1.0));
+      if (splits > 1) t += (splits + 1.0 + extra_planes) * M * N * 4.0 * batch / kHbm + kLaunch;
+      if (t < best * (1.0 - 1e-9)) {
+        best = t;
+        p = {c.bm, c.bn, splits, chunk};
       }
     }
   }
@@ -977,7 +988,7 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
   if (vec && a_kcontig && b_kcontig && M <= 64)
     return skinny_nt(ctx, A, lda, B, ldb, C, ldc, M, N, K, epi);
   // Split-K only pays for long K with few output tiles; used for every form.
-  Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/true);
+  Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/true, 1, epi.mode == EPI_STORE ? 0 : 1);
   GemmArgs a{};
   a.A = A;
   a.B = B;

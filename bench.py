@@ -1,6 +1,6 @@
 """Benchmark of the Aurora GEMM / causal-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only head|sweep]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only LEG]
 
 Workload: one "step" is one pass over the fp32 GEMM sweep
 with M = B·T = 8192 — A@B and A@Bᵀ for (K,N) ∈ {(512,1536), (512,512),
@@ -28,6 +28,7 @@ import numpy as np
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 PEAK_HBM = 8000.0       # GB/s
 
+CLOCK_RAMP_S = 0.25     # untimed sustained work before a timed GEMM region
 COPY_MIB = 256          # calibration copy of the --only traffic leg
 # HBM bytes per head-GEMM launch from the two counter passes of
 # profiles/gemm_head_nt_8192x8192x512_traffic.md: FETCH_SIZE 158034.0 KiB × 2.000
@@ -66,6 +67,99 @@ def build_sweep(ctx, rng):
     items.append(("wgrad_accum_2048x512_t8192", 2.0 * 2048 * 512 * M,
                   lambda: ctx.call("aur_outer_accum", x.ptr, dy.ptr, dest.ptr, 2048, 512, M)))
     return items
+
+
+def gemm_shape_list(m_sweep: int, m_c3: int) -> list[tuple[str, str, int, int, int]]:
+    """(group, form, M or d_out, N or d_in, K or t) of the GEMMs one training
+    step runs.  Group "c1": the config-1 sweep at M = m_sweep rows.  Group
+    "c3": the config-3 (d_model 1024) training GEMMs at M = m_c3 rows —
+    forward A@Bᵀ (fused QKV, W_o, fc, proj, tied head), backward dX = dY·W
+    (A@B) and the weight-gradient accumulates dest += dYᵀ·X (form "acc":
+    d_out, d_in, t)."""
+    out = []
+    for k, n in SWEEP_KN:
+        out.append(("c1", "nn", m_sweep, n, k))
+        out.append(("c1", "nt", m_sweep, n, k))
+    out.append(("c1", "nt", m_sweep, 8192, 512))
+    out.append(("c1", "acc", 2048, 512, m_sweep))
+    d, F, V = C3["d_model"], C3["d_ff"], C3["vocab"]
+    lin = [("qkv", 3 * d, d), ("w_o", d, d), ("fc", F, d), ("proj", d, F), ("head", V, d)]
+    for _, n_out, n_in in lin:
+        out.append(("c3", "nt", m_c3, n_out, n_in))
+    for _, n_out, n_in in lin:
+        out.append(("c3", "nn", m_c3, n_in, n_out))
+    for _, n_out, n_in in lin:
+        out.append(("c3", "acc", n_out, n_in, m_c3))
+    return out
+
+
+def bench_shapes(ctx, steps: int, m_sweep: int, m_c3: int, groups=("c1", "c3")) -> list[dict]:
+    """TFLOP/s of every GEMM of gemm_shape_list(m_sweep, m_c3) in `groups`,
+    each timed alone with HIP events after a warm-up (inputs U(-1,1), resident)."""
+    from aurora_amd.gpu import GpuBuffer
+
+    shapes = [s for s in gemm_shape_list(m_sweep, m_c3) if s[0] in groups]
+
+    def need(form, a, b, c):
+        if form == "acc":  # x [t, d_in], dy [t, d_out], dest [d_out, d_in]
+            return c * b, c * a, a * b
+        return a * c, b * c, a * b
+
+    na = max(need(*s[1:])[0] for s in shapes)
+    nb = max(need(*s[1:])[1] for s in shapes)
+    nc = max(need(*s[1:])[2] for s in shapes)
+    rng = np.random.default_rng(3)
+    bufs = [GpuBuffer.from_slice(ctx, (2 * rng.random(n, dtype=np.float32) - 1)) for n in (na, nb, nc)]
+    pa, pb, pc = (b.ptr for b in bufs)
+    first = shapes[0]
+    ramp_end = time.perf_counter() + CLOCK_RAMP_S
+    while time.perf_counter() < ramp_end:  # clock ramp (see main)
+        for _ in range(10):
+            if first[1] == "acc":
+                ctx.call("aur_outer_accum", pa, pb, pc, first[2], first[3], first[4])
+            else:
+                ctx.call("aur_gemm_nn" if first[1] == "nn" else "aur_gemm_nt", pa, pb, pc, *first[2:])
+        ctx.sync()
+    res = []
+    for group, form, a, b, c in shapes:
+        if form == "acc":
+            fn = lambda a=a, b=b, c=c: ctx.call("aur_outer_accum", pa, pb, pc, a, b, c)
+            name = f"acc_{a}x{b}_t{c}"
+        else:
+            sym = "aur_gemm_nn" if form == "nn" else "aur_gemm_nt"
+            fn = lambda sym=sym, a=a, b=b, c=c: ctx.call(sym, pa, pb, pc, a, b, c)
+            name = f"{form}_{a}x{b}x{c}"
+        for _ in range(3):
+            fn()
+        ms = time_region(ctx, fn, steps)
+        tf = 2.0 * a * b * c / (ms * 1e-3) / 1e12
+        res.append({"group": group, "gemm": name, "ms": round(ms, 4), "tflops": round(tf, 2),
+                    "pct_peak": round(100 * tf / PEAK_FP32_MFMA, 1)})
+        log(f"[bench]   {group} {name:28s} {ms:8.4f} ms {tf:7.1f} TFLOP/s {100 * tf / PEAK_FP32_MFMA:5.1f}%")
+    for x in bufs:
+        x.free()
+    return res
+
+
+def shapes_summary(rows: list[dict], group: str) -> dict:
+    sel = [r for r in rows if r["group"] == group]
+    ms = sum(r["ms"] for r in sel)
+    fl = sum(r["tflops"] * 1e12 * r["ms"] * 1e-3 for r in sel)
+    return {"n_gemms": len(sel), "total_ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+            "min_pct_peak": min(r["pct_peak"] for r in sel),
+            "pct_peak": round(100 * fl / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA, 1)}
+
+
+def bench_c3_and_shards(ctx, steps: int) -> dict:
+    """The config-3 training GEMMs at full size (M = B·T = 16384, the shapes the
+    ≥ 60 % target is stated on) and one GPU's share of both workloads under
+    8-way data parallelism (config 1 at M = 1024 rows, config 3 at M = 2048,
+    weight-gradient t likewise)."""
+    full = bench_shapes(ctx, steps, M, 16384, groups=("c3",))
+    shard = bench_shapes(ctx, steps, M // 8, 16384 // 8)
+    return {"c3_gemms": {**shapes_summary(full, "c3"), "per": full},
+            "dp8_shard": {"c1_m1024": shapes_summary(shard, "c1"), "c3_m2048": shapes_summary(shard, "c3"),
+                          "per": shard}}
 
 
 def time_region(ctx, fn, steps: int) -> float:
@@ -261,7 +355,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["head", "sweep", "train", "decode", "attention", "traffic"],
+    ap.add_argument("--only", choices=["head", "sweep", "train", "decode", "attention", "traffic", "shapes"],
                     default=None,
                     help="profile helper: time only this part and skip the CPU baseline")
     ap.add_argument("--decode-steps", type=int, default=256)
@@ -283,6 +377,11 @@ def main() -> int:
     head = [it for it in items if it[0].startswith("head")][0]
 
     if args.only == "head":
+        ramp_end = time.perf_counter() + CLOCK_RAMP_S
+        while time.perf_counter() < ramp_end:  # clock ramp (see below)
+            for _ in range(10):
+                head[2]()
+            ctx.sync()
         for _ in range(args.warmup):
             head[2]()
         ms = time_region(ctx, head[2], args.steps)
@@ -311,11 +410,23 @@ def main() -> int:
     if args.only == "attention":
         bench_attention(ctx, args.steps)
         return 0
+    if args.only == "shapes":
+        bench_c3_and_shards(ctx, args.steps)
+        return 0
 
     def step():
         for _, _, fn in items:
             fn()
 
+    # Clock ramp: the GPU leaves its idle clocks only after some ~100 ms of
+    # sustained work (measured: 3 warm-up sweeps → 120.4 TFLOP/s, 100 → 125.7),
+    # so the sweep first runs untimed for CLOCK_RAMP_S of wall time, then the
+    # W warm-up steps, then the K timed steps.
+    ramp_end = time.perf_counter() + CLOCK_RAMP_S
+    while time.perf_counter() < ramp_end:
+        for _ in range(10):
+            step()
+        ctx.sync()
     for _ in range(args.warmup):
         step()
     ctx.sync()
@@ -338,6 +449,7 @@ def main() -> int:
 
     if args.only == "sweep":
         return 0
+    shapes = bench_c3_and_shards(ctx, max(5, args.steps // 2))
     attn = bench_attention(ctx, max(3, args.steps // 4))
     train = bench_train(ctx, max(2, min(args.steps, 5)), min(args.warmup, 2))
     decode = bench_decode(ctx, args.decode_steps)
@@ -363,6 +475,8 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "pct_peak": round(100 * value / PEAK_FP32_MFMA, 2),
         "sweep": per,
+        "c3_gemms": shapes["c3_gemms"],
+        "dp8_shard": shapes["dp8_shard"],
         "attention": attn,
         "train": train,
         "decode": decode,
