@@ -368,22 +368,26 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
 // bank conflicts are avoided by an XOR swizzle of 16-byte granules:
 //   k-contiguous operand, [ROWS][32]: granule q of row r at q ^ ((r >> 1) & 7)
 //     (a b128 fragment read of rows r..r+15 at one k hits 16 distinct bank
-//     groups: row parity × the 8 swizzle values);
-//   k-strided operand, [32][ROWS]: granule q of k-row k at q ^ (((k >> 2) & 3) << 2)
+//     groups: row parity × the 8 swizzle values); [ROWS][16] (BK = 16, 64-byte
+//     rows): q ^ ((r >> 2) & 3) (r mod 4 picks the bank quarter, r >> 2 the
+//     granule within it);
+//   k-strided operand, [BK][ROWS]: granule q of k-row k at q ^ (((k >> 2) & 3) << 2)
 //     (the four k-rows 4g + s of a b32 fragment read land in 4 different
 //     granule groups).
 // The swizzle is an involution, so the same function maps physical → logical
 // on the load side.
-template <int ROWS, bool KCONTIG>
+template <int ROWS, bool KCONTIG, int BK = 32>
 struct DirectTile {
-  static constexpr int ELEMS = ROWS * 32;
-  static constexpr int GPR = KCONTIG ? 8 : ROWS / 4;       // 16-byte granules per LDS row
+  static_assert(BK == 32 || BK == 16, "BK is 16 or 32");
+  static constexpr int ELEMS = ROWS * BK;
+  static constexpr int GPR = KCONTIG ? BK / 4 : ROWS / 4;  // 16-byte granules per LDS row
   static constexpr int RPI = 64 / GPR;                     // LDS rows per wave instruction
-  static constexpr int NIW = (KCONTIG ? ROWS : 32) / RPI / 4;  // instructions per wave
-  static_assert(NIW >= 1, "tile too small for four waves");
+  static constexpr int NIW = (KCONTIG ? ROWS : BK) / RPI / 4;  // instructions per wave
+  static_assert(NIW >= 1 && (KCONTIG ? ROWS : BK) % (RPI * 4) == 0, "tile too small for four waves");
 
   __device__ static __forceinline__ int phys(int lrow, int q) {
-    return KCONTIG ? q ^ ((lrow >> 1) & 7) : q ^ (((lrow >> 2) & 3) << 2);
+    if (KCONTIG) return BK == 32 ? q ^ ((lrow >> 1) & 7) : q ^ ((lrow >> 2) & 3);
+    return q ^ (((lrow >> 2) & 3) << 2);
   }
   // This wave's share of the tile at (row origin r0, k origin k0).
   __device__ static __forceinline__ void issue(const float* __restrict__ x, int ld, int r0, int k0,
@@ -402,7 +406,7 @@ struct DirectTile {
   __device__ static __forceinline__ floatx4 frag(const float* __restrict__ lds, int row, int c, int g) {
     floatx4 f;
     if (KCONTIG) {
-      f = *reinterpret_cast<const floatx4*>(lds + row * 32 + 4 * phys(row, 4 * c + g));
+      f = *reinterpret_cast<const floatx4*>(lds + row * BK + 4 * phys(row, 4 * c + g));
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -418,11 +422,17 @@ struct DirectTile {
 // residual R (EPI_RESID) or the activation X (EPI_GELU_BWD) of this wave's
 // tile is loaded into registers with the last K step, so its HBM latency
 // hides under the final MFMAs instead of stalling the store.
-template <int BM, int BN, bool AK, bool BKC, int PRE = 0>
-__global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
+//
+// BK: K per LDS stage.  The 256×128 tile uses BK = 16 (48 KB of LDS for both
+// stages, so two blocks share a CU) and its 128 accumulators per lane must fit
+// beside the fragments in the 256 registers of two waves per SIMD.  Its waves
+// each own 128×64 outputs: 6 load instructions per 128 MFMAs instead of 8,
+// and 12 fragment reads per 32 MFMAs instead of 8 per 16.
+template <int BM, int BN, bool AK, bool BKC, int PRE = 0, int BK = 32>
+__global__ void __launch_bounds__(kThreads, (BM == 256 ? 2 : 1)) gemm_f32_mfma_direct(GemmArgs g) {
   select_batch(g);
-  using TA = DirectTile<BM, AK>;
-  using TB = DirectTile<BN, BKC>;
+  using TA = DirectTile<BM, AK, BK>;
+  using TB = DirectTile<BN, BKC, BK>;
   constexpr int ST = TA::ELEMS + TB::ELEMS;
   constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
   __shared__ __attribute__((aligned(1024))) float smem[2 * ST];
@@ -439,7 +449,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
   const int gsz = min(g.tiles_m - first_m, GM);
   const int m0 = (first_m + (pid % per_group) % gsz) * BM, n0 = ((pid % per_group) / gsz) * BN;
   const int kbeg = blockIdx.z * g.k_chunk;
-  const int nk = (min(g.K, kbeg + g.k_chunk) - kbeg) / 32;
+  const int nk = (min(g.K, kbeg + g.k_chunk) - kbeg) / BK;
 
   floatx4 acc[TM][TN];
 #pragma unroll
@@ -459,14 +469,14 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma_direct(GemmArgs g) {
     const float* sb = sa + TA::ELEMS;
     if (kt + 1 < nk) {  // the other stage was released by the previous barrier
       float* na = smem + ((kt + 1) & 1) * ST;
-      const int k0 = kbeg + (kt + 1) * 32;
+      const int k0 = kbeg + (kt + 1) * BK;
       TA::issue(g.A, g.lda, m0, k0, na, wave, lane);
       TB::issue(g.B, g.ldb, n0, k0, na + TA::ELEMS, wave, lane);
     }
     if constexpr (PRE != 0)
       if (kt == nk - 1) load_epi_operand(g, pre, m0 + wm * WM, n0 + wn * WN, g16, l16, PRE);
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int c = 0; c < BK / 16; ++c) {
       floatx4 fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) fa[i] = TA::frag(sa, wm * WM + i * 16 + l16, c, g16);
@@ -788,8 +798,13 @@ constexpr int kBK = 32;
 // 0.95 / 0.85 (128×128 / 128×64 / 64×64), single-block factor 0.8 / 0.7 /
 // 0.7, 3 TB/s for the reduction and 2 µs per launch; the pick is within 1 %
 // of the measured best on all but one (a 1024×512×512 GEMM, 7 %).
+//
+// allow_wide admits the 256×128 tile (direct-load kernel only: whole tiles,
+// aligned operands, A k-contiguous — with A k-strided it measured 4 % slower
+// than 128×128 — and no prefetched epilogue operand): 1.03 relative
+// efficiency (NT 8192×8192×512: 135.8 vs 130.7 TFLOP/s), 0.75 when alone on a CU.
 Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int batch = 1,
-                 int extra_planes = 0) {
+                 int extra_planes = 0, bool allow_wide = false) {
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   constexpr double kCuFlops = 256.0 * 2.4e9;  // FLOP/s per CU, fp32 MFMA
   constexpr double kHbm = 3.0e12, kLaunch = 2.0e-6;
@@ -797,10 +812,12 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int 
     int bm, bn;
     double eff, single;
   };
-  static constexpr Cand cands[] = {{128, 128, 1.00, 0.8}, {128, 64, 0.95, 0.7}, {64, 64, 0.85, 0.7}};
+  static constexpr Cand cands[] = {
+      {256, 128, 1.03, 0.75}, {128, 128, 1.00, 0.8}, {128, 64, 0.95, 0.7}, {64, 64, 0.85, 0.7}};
   Plan p{128, 128, 1, K};
   double best = 1e30;
   for (const Cand& c : cands) {
+    if (c.bm == 256 && !allow_wide) continue;
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
     for (int s = 1; s <= 16; s *= 2) {
       if (s > 1 && (!allow_split || K / s < 512)) break;
@@ -822,7 +839,8 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int 
   if (const char* env = std::getenv("AUR_GEMM_CFG")) {
     int bm = 0, bn = 0, sp = 1;
     if (std::sscanf(env, "%dx%d:%d", &bm, &bn, &sp) >= 2 &&
-        ((bm == 128 && bn == 128) || (bm == 128 && bn == 64) || (bm == 64 && bn == 64))) {
+        ((bm == 128 && bn == 128) || (bm == 128 && bn == 64) || (bm == 64 && bn == 64) ||
+         (bm == 256 && bn == 128 && allow_wide))) {
       p.bm = bm;
       p.bn = bn;
       if (!allow_split) sp = 1;
@@ -839,6 +857,10 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int 
 template <int BM, int BN, bool AK, bool BKC>
 void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int batch) {
   dim3 grid(a.tiles_m * a.tiles_n, batch, splits);
+  if constexpr (BM == 256) {  // whole tiles only: the planner's allow_wide condition
+    hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, 0, 16>), grid, dim3(kThreads), 0, st, a);
+    return;
+  }
   const bool whole = vec && a.M % BM == 0 && a.N % BN == 0 && a.K % 32 == 0 && a.k_chunk % 32 == 0;
   if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr) {
     if constexpr (BM == 128 && BN == 128) {
@@ -863,6 +885,9 @@ void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int ba
 
 template <bool AK, bool BKC>
 void launch_layout(const GemmArgs& a, const Plan& p, bool vec, hipStream_t st, int batch = 1) {
+  if constexpr (AK) {
+    if (p.bm == 256) return launch_tile<256, 128, AK, BKC>(a, p.splits, vec, st, batch);
+  }
   if (p.bm == 128 && p.bn == 128)
     launch_tile<128, 128, AK, BKC>(a, p.splits, vec, st, batch);
   else if (p.bm == 128 && p.bn == 64)
@@ -988,7 +1013,9 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
   if (vec && a_kcontig && b_kcontig && M <= 64)
     return skinny_nt(ctx, A, lda, B, ldb, C, ldc, M, N, K, epi);
   // Split-K only pays for long K with few output tiles; used for every form.
-  Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/true, 1, epi.mode == EPI_STORE ? 0 : 1);
+  const bool wide = vec && a_kcontig && M % 256 == 0 && N % 128 == 0 && K % 32 == 0 &&
+                    epi.mode != EPI_RESID && epi.mode != EPI_GELU_BWD;
+  Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/true, 1, epi.mode == EPI_STORE ? 0 : 1, wide);
   GemmArgs a{};
   a.A = A;
   a.B = B;
@@ -1041,7 +1068,8 @@ int gemm_batched(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, i
   const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) && (sA % 4 == 0) &&
                    (sB % 4 == 0) && (a_kcontig ? (K % 4 == 0) : (M % 4 == 0)) &&
                    (b_kcontig ? (K % 4 == 0) : (N % 4 == 0));
-  const Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/false, batch);
+  const bool wide = vec && a_kcontig && M % 256 == 0 && N % 128 == 0 && K % 32 == 0;
+  const Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/false, batch, 0, wide);
   GemmArgs a{};
   a.A = A; a.B = B; a.C = C; a.M = M; a.N = N; a.K = K;
   a.lda = lda; a.ldb = ldb; a.ldc = ldc;
