@@ -31,9 +31,9 @@ PEAK_HBM = 8000.0       # GB/s
 CLOCK_RAMP_S = 0.25     # untimed sustained work before a timed GEMM region
 COPY_MIB = 256          # calibration copy of the --only traffic leg
 # HBM bytes per head-GEMM launch from the two counter passes of
-# profiles/gemm_head_nt_8192x8192x512_traffic.md: FETCH_SIZE 158034.0 KiB × 2.000
-# + WRITE_SIZE 262144.8 KiB × 1.000 (factors from the 256 MiB copy).
-HEAD_TRAFFIC_BYTES = (158034.0 * 2.000 + 262144.8 * 1.000) * 1024
+# profiles/gemm_head_nt_8192x8192x512_traffic.md: FETCH_SIZE 108751.9 KiB × 2.000
+# + WRITE_SIZE 262156.3 KiB × 1.000 (factors from the 256 MiB copy).
+HEAD_TRAFFIC_BYTES = (108751.9 * 2.000 + 262156.3 * 1.000) * 1024
 SWEEP_KN = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
 M = 8192
 
@@ -480,7 +480,7 @@ def main() -> int:
         "attention": attn,
         "train": train,
         "decode": decode,
-        "roofline": {"bound": "mfma", "kernel": "gemm_f32_mfma_direct<128,128> (tied head, NT 8192x8192x512)",
+        "roofline": {"bound": "mfma", "kernel": "gemm_f32_mfma_direct<256,128> (tied head, NT 8192x8192x512)",
                      "achieved": round(head_tf, 3), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(head_tf / PEAK_FP32_MFMA, 4), "traffic": round(HEAD_TRAFFIC_BYTES),
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
