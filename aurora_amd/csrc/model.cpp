@@ -42,6 +42,9 @@ struct Carver {
 };
 
 inline void ck(aur_ctx* ctx, int rc, const char* what) { check(ctx, rc, what); }
+inline void hip_ck(aur_ctx* ctx, hipError_t e, const char* what) {
+  if (e != hipSuccess) check(ctx, aur::set_error(ctx, (int)e, "%s: %s", what, hipGetErrorString(e)), what);
+}
 
 // K ranges of the decode QKV projection (K = d_model): ranges of 128, at most
 // 8, tiling K the way gemm_nt_partials does (multiples of 64).
@@ -74,6 +77,13 @@ struct DecoderTransformerGpu::Acts {
   int32_t *csr_off, *csr_idx;
   float *w_tok, *w_pos, *lnf_g, *lnf_b, *g_w_tok, *g_w_pos, *g_lnf_g, *g_lnf_b;
   std::vector<float> nll_host;
+  // Pinned host staging of a training step's uploads (token ids, targets and
+  // the embedding-gradient scatter plan), so they are copied asynchronously
+  // and the plan is built on the host while the GPU runs the forward.
+  // pin_done: recorded after the last copy out of it.
+  uint32_t *pin = nullptr, *pin_tok = nullptr, *pin_tgt = nullptr, *pin_csr_tok = nullptr;
+  int32_t *pin_csr_off = nullptr, *pin_csr_idx = nullptr;
+  hipEvent_t pin_done = nullptr;
 };
 
 DecoderTransformerGpu::DecoderTransformerGpu(aur_ctx* ctx, const TransformerConfig& cfg,
@@ -204,11 +214,22 @@ DecoderTransformerGpu::DecoderTransformerGpu(aur_ctx* ctx, const TransformerConf
   A.csr_off = cv.take<int32_t>(M + 1);
   A.csr_idx = cv.take<int32_t>(M);
   if (cv.off > bytes) throw Error("DecoderTransformerGpu: arena overflow", AUR_ENOMEM);
+  if (hipHostMalloc(reinterpret_cast<void**>(&A.pin), (5 * M + 1) * sizeof(uint32_t)) != hipSuccess)
+    throw Error("DecoderTransformerGpu: pinned staging allocation failed", AUR_ENOMEM);
+  A.pin_tok = A.pin;
+  A.pin_tgt = A.pin + M;
+  A.pin_csr_tok = A.pin + 2 * M;
+  A.pin_csr_idx = reinterpret_cast<int32_t*>(A.pin + 3 * M);
+  A.pin_csr_off = reinterpret_cast<int32_t*>(A.pin + 4 * M);
+  if (hipEventCreateWithFlags(&A.pin_done, hipEventDisableTiming) != hipSuccess)
+    throw Error("DecoderTransformerGpu: event creation failed", AUR_ENOMEM);
 }
 
 DecoderTransformerGpu::~DecoderTransformerGpu() {
   if (ctx_) {
     aur_sync(ctx_);
+    if (acts_ && acts_->pin) (void)hipHostFree(acts_->pin);
+    if (acts_ && acts_->pin_done) (void)hipEventDestroy(acts_->pin_done);
     aur_free(ctx_, act_mem_);
     aur_free(ctx_, state_mem_);
     if (muon_mem_) aur_free(ctx_, muon_mem_);
@@ -363,31 +384,46 @@ float DecoderTransformerGpu::train_step_batch(const uint32_t* tokens, const uint
   if (b > max_batch_ || t > cfg_.seq_len_max) throw Error("train_step_batch: batch/seq too large", AUR_ELIMIT);
   auto& A = *acts_;
   const size_t M = (size_t)b * t;
-  upload_tokens(tokens, targets, b, t);
-  // Embedding-gradient scatter plan: rows grouped by token id, ascending.
-  std::vector<int32_t> idx(M);
-  std::iota(idx.begin(), idx.end(), 0);
-  std::stable_sort(idx.begin(), idx.end(), [&](int32_t x, int32_t y) { return tokens[x] < tokens[y]; });
-  std::vector<uint32_t> uniq;
-  std::vector<int32_t> off;
+  for (size_t i = 0; i < M; ++i)
+    if (tokens[i] >= cfg_.vocab || targets[i] >= cfg_.vocab)
+      throw Error("token or target id out of vocab", AUR_EINVAL);
+  hipStream_t st = ctx_->stream;
+  // The staging area is free once the previous step's copies out of it ran.
+  hip_ck(ctx_, hipEventSynchronize(A.pin_done), "train_step_batch: staging wait");
+  std::memcpy(A.pin_tok, tokens, M * 4);
+  std::memcpy(A.pin_tgt, targets, M * 4);
+  hip_ck(ctx_, hipMemcpyAsync(A.tok, A.pin_tok, M * 4, hipMemcpyHostToDevice, st), "upload tokens");
+  hip_ck(ctx_, hipMemcpyAsync(A.tgt, A.pin_tgt, M * 4, hipMemcpyHostToDevice, st), "upload targets");
+  encode_forward(b, t, nullptr, true);
+  // While the GPU runs the forward: the embedding-gradient scatter plan
+  // (rows grouped by token id, ascending; stable within a token), uploaded
+  // behind the forward on the same stream, ahead of the backward that reads it.
+  int32_t* idx = A.pin_csr_idx;
+  std::iota(idx, idx + M, 0);
+  std::stable_sort(idx, idx + M, [&](int32_t x, int32_t y) { return tokens[x] < tokens[y]; });
+  size_t nuniq = 0;
   for (size_t i = 0; i < M; ++i) {
     if (i == 0 || tokens[idx[i]] != tokens[idx[i - 1]]) {
-      uniq.push_back(tokens[idx[i]]);
-      off.push_back((int32_t)i);
+      A.pin_csr_tok[nuniq] = tokens[idx[i]];
+      A.pin_csr_off[nuniq] = (int32_t)i;
+      ++nuniq;
     }
   }
-  off.push_back((int32_t)M);
-  ck(ctx_, aur_h2d(ctx_, A.csr_tok, uniq.data(), uniq.size() * 4), "csr tok");
-  ck(ctx_, aur_h2d(ctx_, A.csr_off, off.data(), off.size() * 4), "csr off");
-  ck(ctx_, aur_h2d(ctx_, A.csr_idx, idx.data(), M * 4), "csr idx");
+  A.pin_csr_off[nuniq] = (int32_t)M;
+  auto up = [&](void* dst, const void* src, size_t bytes, const char* what) {
+    hip_ck(ctx_, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st), what);
+  };
+  up(A.csr_tok, A.pin_csr_tok, nuniq * 4, "csr tok");
+  up(A.csr_off, A.pin_csr_off, (nuniq + 1) * 4, "csr off");
+  up(A.csr_idx, A.pin_csr_idx, M * 4, "csr idx");
+  hip_ck(ctx_, hipEventRecord(A.pin_done, st), "train_step_batch: staging event");
 
-  encode_forward(b, t, nullptr, true);
   // CE with 1/T per sequence and the batch mean folded into one scale.
   ck(ctx_, aur::softmax_ce(ctx_, A.logits, A.tgt, A.nll, (int)M, (int)cfg_.vocab, 1.0f / ((float)t * b)),
      "softmax_ce");
   encode_backward(b, t);
   ck(ctx_, aur::embed_backward(ctx_, A.dx_a, (int)b, (int)t, (int)cfg_.d_model, A.csr_tok, A.csr_off, A.csr_idx,
-                               (int)uniq.size(), A.g_w_tok, A.g_w_pos),
+                               (int)nuniq, A.g_w_tok, A.g_w_pos),
      "embed bwd");
   A.nll_host.resize(M);
   ck(ctx_, aur_d2h(ctx_, A.nll_host.data(), A.nll, M * 4), "download nll");
