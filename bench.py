@@ -309,8 +309,11 @@ def bench_attention(ctx, steps: int) -> dict:
     fwd, bwd = CausalMhaForwardKernel(), CausalMhaBackwardKernel()
     f = lambda: fwd.dispatch_into(ctx, q, k, v, o, lse, T, H, dh, b=B)
     g = lambda: bwd.dispatch_into(ctx, q, k, v, o, lse, do, dq, dk, dv, ws, T, H, dh, b=B)
-    f()
-    g()
+    ramp_end = time.perf_counter() + CLOCK_RAMP_S
+    while time.perf_counter() < ramp_end:  # clock ramp, as before the GEMM sweep
+        f()
+        g()
+        ctx.sync()
     ms_f = time_region(ctx, f, steps)
     ms_b = time_region(ctx, g, steps)
     pairs = B * H * T * (T + 1) / 2
