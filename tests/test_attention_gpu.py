@@ -83,6 +83,28 @@ def test_causal_mha_backward_matches_cpu(ctx, t, H, dh):
         assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
 
 
+_RAND_ATTN = [(int(r.integers(1, 4)), int(r.integers(1, 330)), int(r.integers(1, 5)), int(r.choice([8, 16, 32, 64])))
+              for r in (np.random.default_rng(7700 + i) for i in range(8))]
+
+
+@pytest.mark.parametrize("B,t,H,dh", _RAND_ATTN)
+def test_seeded_random_batched_forward_backward(ctx, B, t, H, dh):
+    """8 seeded random (batch, t, heads, d_head): ragged last tiles, every
+    d_head, batch > 1; forward, LSE and all three gradients against float64."""
+    rng = np.random.default_rng(B * 100_003 + t * 101 + H * 7 + dh)
+    n = B * t * H * dh
+    q, k, v, do = (_n(rng, n) for _ in range(4))
+    out, lse = _fwd(ctx, q, k, v, B, t, H, dh)
+    shp = (B, t, H, dh)
+    o64, l64 = causal_attention_f64(*(x.reshape(shp).astype(np.float64) for x in (q, k, v)))
+    assert fro_rel(out, o64) < TOL_ATTN and max_norm_rel(out, o64) < TOL_ATTN
+    np.testing.assert_allclose(lse.reshape(B, H, t), l64, rtol=0, atol=1e-4)
+    grads = _bwd(ctx, q, k, v, out, lse, do, B, t, H, dh)
+    g64 = causal_attention_grad_f64(*(x.reshape(shp).astype(np.float64) for x in (q, k, v, do)))
+    for got, want in zip(grads, g64):
+        assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
+
+
 def test_backward_accumulates_and_is_deterministic(ctx):
     B, T, H, dh = 2, 97, 2, 64
     rng = np.random.default_rng(9)

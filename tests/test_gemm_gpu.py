@@ -124,6 +124,29 @@ def test_ragged_shapes_all_forms(ctx, m, k, n):
     assert cw < TOL_GEMM and fr < TOL_GEMM, ("outer", cw, fr)
 
 
+_RAND_SHAPES = [tuple(int(v) for v in np.random.default_rng(9000 + i).integers(1, 700, 3)) for i in range(16)]
+
+
+@pytest.mark.parametrize("m,k,n", _RAND_SHAPES)
+def test_seeded_random_shapes_all_forms(ctx, m, k, n):
+    """16 seeded random (M, K, N) in [1, 700): every tile edge, K tail and
+    scalar/vector load path the planner reaches, all three forms, against
+    float64."""
+    rng = np.random.default_rng(m * 1_000_003 + k * 1009 + n)
+    a = _u(rng, m * k)
+    b_nn, b_nt = _u(rng, k * n), _u(rng, n * k)
+    a64 = a.reshape(m, k).astype(np.float64)
+    cw, fr = _gates(_nn(ctx, a, b_nn, m, n, k), a64, b_nn.reshape(k, n).astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("nn", cw, fr)
+    cw, fr = _gates(_nt(ctx, a, b_nt, m, n, k), a64, b_nt.reshape(n, k).T.astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("nt", cw, fr)
+    x, dy, dest = _u(rng, k * n), _u(rng, k * m), _u(rng, m * n)
+    got = _outer(ctx, x, dy, dest, m, n, k)
+    cw, fr = _gates(got, dy.reshape(k, m).T.astype(np.float64), x.reshape(k, n).astype(np.float64),
+                    dest.reshape(m, n))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("outer", cw, fr)
+
+
 @pytest.mark.parametrize("cfg", ["256x128:1", "256x128:2", "128x128:1", "128x128:4", "128x64:1",
                                  "128x64:2", "64x64:1", "64x64:4", "staged"])
 def test_every_tile_config_all_forms(ctx, monkeypatch, cfg):
