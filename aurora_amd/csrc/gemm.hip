@@ -859,8 +859,7 @@ void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int ba
   dim3 grid(a.tiles_m * a.tiles_n, batch, splits);
   if constexpr (BM == 256) {  // whole tiles only: the planner's allow_wide condition
     hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, 0, 16>), grid, dim3(kThreads), 0, st, a);
-    return;
-  }
+  } else {
   const bool whole = vec && a.M % BM == 0 && a.N % BN == 0 && a.K % 32 == 0 && a.k_chunk % 32 == 0;
   if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr) {
     if constexpr (BM == 128 && BN == 128) {
@@ -881,6 +880,7 @@ void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int ba
     hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, kBK, AK, BKC, true>), grid, dim3(kThreads), 0, st, a);
   else
     hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, kBK, AK, BKC, false>), grid, dim3(kThreads), 0, st, a);
+  }
 }
 
 template <bool AK, bool BKC>
