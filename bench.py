@@ -356,6 +356,38 @@ def cpu_baseline(budget_s: float = 10.0) -> dict:
                       f"1/8 of its rows) x{reps} in {el:.1f}s, 64-row sequences over {threads} threads"}
 
 
+def cpu_decode_sample(n_steps: int = 6) -> dict:
+    """The reference CPU decode path (kv_cache.rs generate_step, restated in
+    oracle/model.py) on the config-4 model for ONE sequence, single-threaded,
+    with its KV cache pre-filled to 640 positions (the average length of the
+    256-step C4 run; the step's cost does not depend on the cached values).
+    The reference runs the 32 sequences in parallel over the host's cores
+    (rayon), so tok/s at C cores ≈ C / (seconds per step)."""
+    from oracle import model as om
+
+    cfg = om.Config(vocab=C3["vocab"], d_model=C3["d_model"], n_layer=C3["n_layer"], n_head=C3["n_head"],
+                    d_ff=C3["d_ff"], seq_len_max=768 + 64)
+    P = om.init_params(cfg, 2)
+    rng = np.random.default_rng(5)
+    kv = om.KvCache(cfg)
+    t0 = 640
+    for l in range(cfg.n_layer):
+        kv.k[l] = rng.standard_normal(t0 * cfg.d_model, dtype=np.float32)
+        kv.v[l] = rng.standard_normal(t0 * cfg.d_model, dtype=np.float32)
+    kv.current_len = t0
+    tok = 17
+    om.generate_step(P, cfg, kv, tok)  # warm-up
+    t_start = time.perf_counter()
+    for _ in range(n_steps):
+        tok = om.argmax(om.generate_step(P, cfg, kv, tok))
+    sec = (time.perf_counter() - t_start) / n_steps
+    cores = min(16, len(os.sched_getaffinity(0)))
+    return {"s_per_token_1core": round(sec, 4), "cores": cores, "tok_per_s_est": round(cores / sec, 1),
+            "sample": f"oracle generate_step, config-4 model, one sequence at KV length {t0}..{t0 + n_steps}, "
+                      f"{n_steps} steps single-threaded; tok_per_s_est = cores / s_per_token (the reference "
+                      f"decodes sequences in parallel)"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -460,6 +492,9 @@ def main() -> int:
     train = bench_train(ctx, max(2, min(args.steps, 5)), min(args.warmup, 2))
     decode = bench_decode(ctx, args.decode_steps)
     cpu = cpu_baseline(args.cpu_budget)
+    # The same leg also times the reference CPU decode step (config 4).
+    cpu["decode"] = cpu_decode_sample()
+    cpu["decode"]["gpu_speedup"] = round(decode["tok_per_s"] / cpu["decode"]["tok_per_s_est"], 1)
     log(f"[bench] cpu baseline {cpu}")
 
     line = {
