@@ -388,6 +388,44 @@ def cpu_decode_sample(n_steps: int = 6) -> dict:
                       f"decodes sequences in parallel)"}
 
 
+def cpu_train_sample(t: int = 32) -> dict:
+    """The reference CPU training path (forward, CE, backward, clip, AdamW —
+    oracle/model.py restating model.rs / optimizer.rs) on the config-3 model
+    for ONE sequence of t tokens, single-threaded, timed once after a warm-up.
+    The reference computes a batch's per-sequence gradients in parallel
+    (rayon), so a config-3 step (16 × 1024 tokens) over C cores is estimated
+    as forward+backward per token × 16384 / C × (1 + 0.09) — the linear and
+    head FLOP scale with tokens, causal attention adds 1.44 of 15.67 TFLOP at
+    T = 1024 (≈ 0 at t) — plus the clip + AdamW pass once."""
+    from oracle import model as om
+
+    cfg = om.Config(vocab=C3["vocab"], d_model=C3["d_model"], n_layer=C3["n_layer"], n_head=C3["n_head"],
+                    d_ff=C3["d_ff"], seq_len_max=C3["seq_len_max"])
+    P = om.init_params(cfg, 2)
+    rng = np.random.default_rng(6)
+    seq = rng.integers(0, cfg.vocab, (1, t + 1)).astype(np.uint32)
+    tok, tgt = seq[:, :t], seq[:, 1:]
+    state = om.new_adam_state(P)
+
+    def step():
+        t0 = time.perf_counter()
+        _, G = om.batch_grads(P, cfg, tok, tgt)
+        t1 = time.perf_counter()
+        om.clip_grads(G, 1.0)
+        om.step_adamw(P, G, state, lr=3e-4, wd=0.1)
+        return t1 - t0, time.perf_counter() - t1
+
+    step()
+    fb, opt = step()
+    cores = min(16, len(os.sched_getaffinity(0)))
+    est = fb / t * 16 * 1024 / cores * (1.0 + 1.44 / 15.67) + opt
+    return {"s_fwd_bwd_one_seq": round(fb, 3), "s_clip_adamw": round(opt, 3), "tokens": t, "cores": cores,
+            "c3_step_s_est": round(est, 1),
+            "sample": f"oracle batch_grads, then clip + AdamW, config-3 model, one sequence of {t} tokens, "
+                      f"single-threaded; c3_step_s_est = forward+backward per token x 16 x 1024 tokens over "
+                      f"the cores (+9 % causal attention at T = 1024) + clip + AdamW once"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -495,6 +533,8 @@ def main() -> int:
     # The same leg also times the reference CPU decode step (config 4).
     cpu["decode"] = cpu_decode_sample()
     cpu["decode"]["gpu_speedup"] = round(decode["tok_per_s"] / cpu["decode"]["tok_per_s_est"], 1)
+    cpu["train"] = cpu_train_sample()
+    cpu["train"]["gpu_speedup"] = round(cpu["train"]["c3_step_s_est"] / (train["ms_per_step"] * 1e-3), 1)
     log(f"[bench] cpu baseline {cpu}")
 
     line = {
