@@ -1014,7 +1014,8 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
     return skinny_nt(ctx, A, lda, B, ldb, C, ldc, M, N, K, epi);
   // Split-K only pays for long K with few output tiles; used for every form.
   const bool wide = vec && a_kcontig && M % 256 == 0 && N % 128 == 0 && K % 32 == 0 &&
-                    epi.mode != EPI_RESID && epi.mode != EPI_GELU_BWD;
+                    epi.mode != EPI_RESID && epi.mode != EPI_GELU_BWD &&
+                    std::getenv("AUR_GEMM_STAGED") == nullptr;
   Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/true, 1, epi.mode == EPI_STORE ? 0 : 1, wide);
   GemmArgs a{};
   a.A = A;
@@ -1068,7 +1069,8 @@ int gemm_batched(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, i
   const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) && (sA % 4 == 0) &&
                    (sB % 4 == 0) && (a_kcontig ? (K % 4 == 0) : (M % 4 == 0)) &&
                    (b_kcontig ? (K % 4 == 0) : (N % 4 == 0));
-  const bool wide = vec && a_kcontig && M % 256 == 0 && N % 128 == 0 && K % 32 == 0;
+  const bool wide = vec && a_kcontig && M % 256 == 0 && N % 128 == 0 && K % 32 == 0 &&
+                    std::getenv("AUR_GEMM_STAGED") == nullptr;
   const Plan p = choose_plan(ctx, M, N, K, /*allow_split=*/false, batch, 0, wide);
   GemmArgs a{};
   a.A = A; a.B = B; a.C = C; a.M = M; a.N = N; a.K = K;
