@@ -27,6 +27,8 @@
 // DH = 8 the upper half of the single chunk is zero.
 #include "common.hpp"
 
+#include <cstdlib>
+
 namespace {
 
 constexpr int TQ = 64;  // rows per tile (4 waves × 16)
@@ -251,6 +253,148 @@ __global__ void __launch_bounds__(256) mha_fwd_kernel(AttnArgs a) {
     for (int d = 0; d < NC; ++d)
       if (G::live(16 * d + 4 * g))
         *reinterpret_cast<floatx4*>(orow + 16 * d + 4 * g) = acc_o[d] * inv;
+    if (g == 0) a.lse[((size_t)b * a.H + h) * a.T + qrow] = (m + __log2f(l)) * (1.f / LOG2E);
+  }
+}
+
+// Direct-load forward (d_head = 64): K and V tiles go from memory straight
+// into LDS with global_load_lds_dwordx4 (a wave instruction fills 1 KB = four
+// 64-float rows): no staging registers and no ds_write.  One LDS stage
+// (32 KB), so that as many blocks share a CU as with the register-staged
+// kernel; a block's next-tile load latency is covered by the other blocks.
+// The rows are unpadded; XOR swizzles of the 16-byte granules keep the
+// fragment reads conflict-free:
+//   K (b128 reads of 16 consecutive rows at one granule): granule q of row r at q ^ (r & 15);
+//   V (b32 reads of rows 4g + s, 16 consecutive columns):  q ^ (((r >> 2) & 3) << 2).
+// Rows past T are loaded from row T − 1 (finite, and masked: a key ≥ T is
+// always in the future of every query < T).
+template <bool ISK>
+__device__ __forceinline__ int attn_swz(int row, int q) {
+  return ISK ? q ^ (row & 15) : q ^ (((row >> 2) & 3) << 2);
+}
+
+template <bool ISK>
+__device__ __forceinline__ void issue_kv64(const float* __restrict__ base, int ld, int r0, int T, float* lds,
+                                           int w, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int L0 = 4 * (4 * w + j);  // first of the four rows of this instruction
+    const int row = L0 + (lane >> 4);
+    const int q = attn_swz<ISK>(row, lane & 15);
+    const int grow = min(r0 + row, T - 1);
+    __builtin_amdgcn_global_load_lds(base + (size_t)grow * ld + 4 * q,
+                                     (__attribute__((address_space(3))) void*)(lds + L0 * 64), 16, 0, 0);
+  }
+}
+
+template <bool DIAG>
+__device__ __forceinline__ void fwd_tile_direct(const float* __restrict__ Ks, const float* __restrict__ Vs,
+                                                const floatx4* qf, floatx4* acc_o, float& m, float& l,
+                                                int w, int g, int l16) {
+  constexpr int NC = 4;
+  const int jmax = DIAG ? w : 3;
+  floatx4 st[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    st[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (j <= jmax) {
+      const int row = 16 * j + l16;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const floatx4 kf = *reinterpret_cast<const floatx4*>(Ks + row * 64 + 4 * attn_swz<true>(row, 4 * c + g));
+#pragma unroll
+        for (int s = 0; s < 4; ++s) st[j] = mfma16x16x4(kf[s], qf[c][s], st[j]);
+      }
+    }
+  }
+  if (DIAG) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (j > jmax || 16 * j + 4 * g + e > 16 * w + l16) st[j][e] = -INFINITY;
+  }
+  float mx = fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3]));
+#pragma unroll
+  for (int j = 1; j < 4; ++j) mx = fmaxf(mx, fmaxf(fmaxf(st[j][0], st[j][1]), fmaxf(st[j][2], st[j][3])));
+  mx = fmaxf(mx, shfl_xor(mx, 16));
+  mx = fmaxf(mx, shfl_xor(mx, 32));
+  const float m_new = fmaxf(m, mx);
+  const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+  m = m_new;
+  float ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = __builtin_amdgcn_exp2f(st[j][e] - m_new);
+      st[j][e] = p;
+      ps += p;
+    }
+  l = l * alpha + ps;
+#pragma unroll
+  for (int d = 0; d < NC; ++d) acc_o[d] *= alpha;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j <= jmax) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int key = 16 * j + 4 * g + s;
+#pragma unroll
+        for (int d = 0; d < NC; ++d) {
+          const int col = 16 * d + l16;
+          const float v = Vs[key * 64 + 4 * attn_swz<false>(key, col >> 2) + (col & 3)];
+          acc_o[d] = mfma16x16x4(v, st[j][s], acc_o[d]);
+        }
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) mha_fwd_direct_kernel(AttnArgs a) {
+  constexpr int DH = 64, NC = 4, TILE = 64 * 64;
+  __shared__ __attribute__((aligned(1024))) float sm[2][TILE];  // [K, V]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int nqt = (a.T + TQ - 1) / TQ;
+  const int qt = nqt - 1 - blockIdx.z;  // longest query tiles first over the whole launch
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int q0 = qt * TQ;
+  const size_t row_base = (size_t)b * a.T;
+  const float* Qb = a.q + row_base * a.ld_qkv + h * DH;
+  const float* Kb = a.k + row_base * a.ld_qkv + h * DH;
+  const float* Vb = a.v + row_base * a.ld_qkv + h * DH;
+
+  issue_kv64<true>(Kb, a.ld_qkv, 0, a.T, sm[0], w, lane);
+  issue_kv64<false>(Vb, a.ld_qkv, 0, a.T, sm[1], w, lane);
+  const int qrow = q0 + 16 * w + l16;
+  floatx4 qf[NC];
+  load_rows_frag<DH>(qf, Qb, a.ld_qkv, qrow, a.T, g);
+  const float sl2 = a.scale * LOG2E;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) qf[c] *= sl2;
+  float m = -INFINITY, l = 0.f;
+  floatx4 acc_o[NC];
+#pragma unroll
+  for (int d = 0; d < NC; ++d) acc_o[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int kt = 0; kt < qt; ++kt) {
+    fwd_tile_direct<false>(sm[0], sm[1], qf, acc_o, m, l, w, g, l16);
+    __syncthreads();  // every wave is done with the stage
+    issue_kv64<true>(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, sm[0], w, lane);
+    issue_kv64<false>(Vb, a.ld_qkv, (kt + 1) * TQ, a.T, sm[1], w, lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+  fwd_tile_direct<true>(sm[0], sm[1], qf, acc_o, m, l, w, g, l16);
+  l += shfl_xor(l, 16);
+  l += shfl_xor(l, 32);
+  if (qrow < a.T) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    float* orow = a.out + (row_base + qrow) * a.ld_o + h * DH;
+#pragma unroll
+    for (int d = 0; d < NC; ++d) *reinterpret_cast<floatx4*>(orow + 16 * d + 4 * g) = acc_o[d] * inv;
     if (g == 0) a.lse[((size_t)b * a.H + h) * a.T + qrow] = (m + __log2f(l)) * (1.f / LOG2E);
   }
 }
@@ -524,6 +668,12 @@ int check_common(aur_ctx* ctx, uint32_t b, uint32_t t, uint32_t n_head, uint32_t
 template <int DH>
 void launch_fwd(const AttnArgs& a, int b, hipStream_t st) {
   dim3 grid(a.H, b, (a.T + TQ - 1) / TQ);
+  if constexpr (DH == 64) {
+    if (std::getenv("AUR_ATTN_FWD_STAGED") == nullptr) {
+      hipLaunchKernelGGL(mha_fwd_direct_kernel, grid, dim3(256), 0, st, a);
+      return;
+    }
+  }
   hipLaunchKernelGGL((mha_fwd_kernel<DH>), grid, dim3(256), 0, st, a);
 }
 
