@@ -351,7 +351,7 @@ __device__ __forceinline__ void fwd_tile_direct(const float* __restrict__ Ks, co
   }
 }
 
-__global__ void __launch_bounds__(256) mha_fwd_direct_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, 4) mha_fwd_direct_kernel(AttnArgs a) {
   constexpr int DH = 64, NC = 4, TILE = 64 * 64;
   __shared__ __attribute__((aligned(1024))) float sm[2][TILE];  // [K, V]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
