@@ -428,7 +428,7 @@ __global__ void __launch_bounds__(256) mha_bwd_rowdot_kernel(AttnArgs a, int B) 
 
 // ---------------------------------------- backward pass 2: dK, dV (and dS)
 template <int DH, int NS>
-__global__ void __launch_bounds__(256) mha_bwd_dkv_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, (NS == 1 ? 3 : 1)) mha_bwd_dkv_kernel(AttnArgs a) {
   using G = Geo<DH>;
   constexpr int NC = G::NC, LDT = G::LDT;
   __shared__ __attribute__((aligned(16))) float sm[NS][2][G::TILE];  // [stage][Q,dO]
@@ -684,7 +684,10 @@ void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
   hipLaunchKernelGGL(mha_bwd_rowdot_kernel<DH>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256),
                      0, st, a, b);
   dim3 grid(a.H, b, (a.T + TQ - 1) / TQ);
-  hipLaunchKernelGGL((mha_bwd_dkv_kernel<DH, 2>), grid, dim3(256), 0, st, a);  // also stores dS
+  if (std::getenv("AUR_ATTN_DKV_NS2") == nullptr)
+    hipLaunchKernelGGL((mha_bwd_dkv_kernel<DH, 1>), grid, dim3(256), 0, st, a);  // also stores dS
+  else
+    hipLaunchKernelGGL((mha_bwd_dkv_kernel<DH, 2>), grid, dim3(256), 0, st, a);
   hipLaunchKernelGGL((mha_bwd_dq_kernel<DH>), grid, dim3(256), 0, st, a);
 }
 
