@@ -105,6 +105,25 @@ def test_seeded_random_batched_forward_backward(ctx, B, t, H, dh):
         assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
 
 
+@pytest.mark.parametrize("env", ["AUR_ATTN_FWD_STAGED", "AUR_ATTN_DKV_NS2"])
+def test_alternate_kernels_d64(ctx, monkeypatch, env):
+    """The d_head = 64 kernels reachable only through the overrides (register-
+    staged forward, two-stage dK/dV ring) against float64, ragged T, batch 2."""
+    monkeypatch.setenv(env, "1")
+    B, t, H, dh = 2, 201, 3, 64
+    rng = np.random.default_rng(4242 + len(env))
+    n = B * t * H * dh
+    q, k, v, do = (_n(rng, n) for _ in range(4))
+    out, lse = _fwd(ctx, q, k, v, B, t, H, dh)
+    shp = (B, t, H, dh)
+    o64, l64 = causal_attention_f64(*(x.reshape(shp).astype(np.float64) for x in (q, k, v)))
+    assert fro_rel(out, o64) < TOL_ATTN and max_norm_rel(out, o64) < TOL_ATTN
+    grads = _bwd(ctx, q, k, v, out, lse, do, B, t, H, dh)
+    g64 = causal_attention_grad_f64(*(x.reshape(shp).astype(np.float64) for x in (q, k, v, do)))
+    for got, want in zip(grads, g64):
+        assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
+
+
 def test_backward_accumulates_and_is_deterministic(ctx):
     B, T, H, dh = 2, 97, 2, 64
     rng = np.random.default_rng(9)
