@@ -669,6 +669,86 @@ int check_common(aur_ctx* ctx, uint32_t b, uint32_t t, uint32_t n_head, uint32_t
   return 0;
 }
 
+// Direct-load dQ pass (d_head = 64): K tiles go straight into a swizzled,
+// double-buffered LDS ring (granule q of row r at q ^ (((r >> 2) & 3) << 2),
+// conflict-free for the b32 reads of rows 4g + s × 16 columns), no staging
+// registers, one barrier per tile.  K rows past T are loaded from row T − 1: every dS entry
+// of a key ≥ T is zero for the queries < T (pass 2 masks them), so they add
+// nothing.
+__global__ void __launch_bounds__(256, 5) mha_bwd_dq_direct_kernel(AttnArgs a) {
+  constexpr int DH = 64, NC = 4;
+  __shared__ __attribute__((aligned(1024))) float sm[2][64 * 64];  // K tiles
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int nqt = (a.T + TQ - 1) / TQ;
+  const int qt = nqt - 1 - blockIdx.z;  // longest query tiles first (grid H, B, tiles)
+  const int h = blockIdx.x, b = blockIdx.y;
+  const size_t row_base = (size_t)b * a.T;
+  const float* Kb = a.k + row_base * a.ld_qkv + h * DH;
+  const float* tiles = a.ds + (((size_t)b * a.H + h) * a.ntri + qt * (qt + 1) / 2) * (TQ * TQ) +
+                       (16 * w + l16) * TQ + 4 * g;
+  auto load_ds = [&](int kt, floatx4* f) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[j] = *reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + 16 * j);
+  };
+  auto issue_k = [&](int kt, float* lds) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int L0 = 4 * (4 * w + j);
+      const int row = L0 + (lane >> 4);
+      const int q = (lane & 15) ^ (((row >> 2) & 3) << 2);
+      const int grow = min(kt * TQ + row, a.T - 1);
+      __builtin_amdgcn_global_load_lds(Kb + (size_t)grow * a.ld_qkv + 4 * q,
+                                       (__attribute__((address_space(3))) void*)(lds + L0 * 64), 16, 0, 0);
+    }
+  };
+  floatx4 acc[NC];
+#pragma unroll
+  for (int d = 0; d < NC; ++d) acc[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 fc[4], fn[4];
+  issue_k(0, sm[0]);
+  load_ds(0, fc);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int kt = 0; kt <= qt; ++kt) {
+    const bool more = kt < qt;
+    if (more) {  // the other buffer was released by the previous barrier
+      issue_k(kt + 1, sm[(kt + 1) & 1]);
+      load_ds(kt + 1, fn);
+    }
+    const float* Ks = sm[kt & 1];
+    const int jmax = more ? 3 : w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j > jmax) continue;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int r = 16 * j + 4 * g + s;
+#pragma unroll
+        for (int d = 0; d < NC; ++d) {
+          const int col = 16 * d + l16;
+          acc[d] = mfma16x16x4(Ks[r * 64 + 4 * ((col >> 2) ^ (((r >> 2) & 3) << 2)) + (col & 3)], fc[j][s], acc[d]);
+        }
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fc[j] = fn[j];
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+  }
+  const int qrow = qt * TQ + 16 * w + l16;
+  if (qrow < a.T) {
+    float* dqr = a.dq + (row_base + qrow) * a.ld_d + h * DH;
+#pragma unroll
+    for (int d = 0; d < NC; ++d) {
+      floatx4* pq = reinterpret_cast<floatx4*>(dqr + 16 * d + 4 * g);
+      *pq = a.overwrite ? acc[d] * a.scale : *pq + acc[d] * a.scale;
+    }
+  }
+}
+
 template <int DH>
 void launch_fwd(const AttnArgs& a, int b, hipStream_t st) {
   dim3 grid(a.H, b, (a.T + TQ - 1) / TQ);
@@ -692,7 +772,10 @@ void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
     hipLaunchKernelGGL((mha_bwd_dkv_kernel<DH, 1>), grid, dim3(256), 0, st, a);  // also stores dS
   else
     hipLaunchKernelGGL((mha_bwd_dkv_kernel<DH, 2>), grid, dim3(256), 0, st, a);
-  hipLaunchKernelGGL((mha_bwd_dq_kernel<DH>), grid, dim3(256), 0, st, a);
+  if (DH == 64 && std::getenv("AUR_ATTN_DQ_STAGED") == nullptr)
+    hipLaunchKernelGGL(mha_bwd_dq_direct_kernel, grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((mha_bwd_dq_kernel<DH>), grid, dim3(256), 0, st, a);
 }
 
 }  // namespace

@@ -105,10 +105,11 @@ def test_seeded_random_batched_forward_backward(ctx, B, t, H, dh):
         assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
 
 
-@pytest.mark.parametrize("env", ["AUR_ATTN_FWD_STAGED", "AUR_ATTN_DKV_NS2"])
+@pytest.mark.parametrize("env", ["AUR_ATTN_FWD_STAGED", "AUR_ATTN_DKV_NS2", "AUR_ATTN_DQ_STAGED"])
 def test_alternate_kernels_d64(ctx, monkeypatch, env):
     """The d_head = 64 kernels reachable only through the overrides (register-
-    staged forward, two-stage dK/dV ring) against float64, ragged T, batch 2."""
+    staged forward, two-stage dK/dV ring, register-staged dQ) against float64,
+    ragged T, batch 2."""
     monkeypatch.setenv(env, "1")
     B, t, H, dh = 2, 201, 3, 64
     rng = np.random.default_rng(4242 + len(env))
