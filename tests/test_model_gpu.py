@@ -43,6 +43,24 @@ def _compare_tree(got, want, tol, what):
     return worst
 
 
+@pytest.mark.parametrize("vocab", [1024, 2048])
+def test_train_step_row_resident_ce_matches_cpu(ctx, vocab):
+    """Vocabularies that are multiples of 1024 take the row-resident softmax-CE
+    kernel (the C3 head, V = 8192, does too): loss and every gradient against
+    the CPU restatement, including the tied embedding that the CE gradient
+    feeds."""
+    cfg = OM.Config(vocab=vocab, d_model=64, n_layer=1, n_head=2, d_ff=128, seq_len_max=32)
+    P = OM.init_params(cfg, 5)
+    tok, tgt = _tokens(cfg, 4, 32, 5)
+    m = _gpu_model(ctx, cfg, 4, P)
+    m.zero_grad()
+    loss_gpu = m.train_step_batch(tok, tgt)
+    loss_cpu, G = OM.batch_grads(P, cfg, tok, tgt)
+    assert abs(loss_gpu - loss_cpu) < 1e-4 * abs(loss_cpu), (loss_gpu, loss_cpu)
+    _compare_tree(m.read_tensors(grad=True), G, 1e-3, "grad")
+    m.destroy()
+
+
 def test_config0_train_step_matches_cpu(ctx):
     """One forward + backward + clip(1.0) + AdamW(lr 3e-4, wd 0.1) step."""
     cfg = C0
