@@ -367,6 +367,9 @@ __global__ void __launch_bounds__(256) ln_param_partial_kernel(const float* __re
   if (c >= d) return;
   const int r0 = chunk * LN_CHUNK, r1 = min(rows, r0 + LN_CHUNK);
   float sgm = 0.f, sb = 0.f;
+  // Unrolled so that several rows' loads are in flight; the sums still run
+  // in increasing r.
+#pragma unroll 16
   for (int r = r0; r < r1; ++r) {
     const float g = dy[(size_t)r * d + c];
     sgm += g * ((x[(size_t)r * d + c] - mean[r]) * rstd[r]);
