@@ -516,6 +516,24 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ P
   }
 }
 
+// splitk_reduce for N % 4 == 0: four consecutive outputs per thread (float4
+// partial loads, 32-bit index math), the same increasing-z sum per element.
+__global__ void __launch_bounds__(256) splitk_reduce4(const float* __restrict__ P, float* __restrict__ C,
+                                                       int M, int N, int ldc, int splits,
+                                                       aur::Epilogue epi) {
+  const size_t plane = (size_t)M * N;
+  const unsigned total4 = (unsigned)(plane / 4), un = (unsigned)N;
+  for (unsigned i = blockIdx.x * blockDim.x + threadIdx.x; i < total4; i += gridDim.x * blockDim.x) {
+    const unsigned e = 4 * i;
+    floatx4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int z = 0; z < splits; ++z) s += *reinterpret_cast<const floatx4*>(P + (size_t)z * plane + e);
+    const unsigned row = e / un, col = e - row * un;
+    const size_t idx = (size_t)row * ldc + col;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) apply_epilogue(epi, C, idx + k, s[k]);
+  }
+}
+
 // ------------------------------------------------------------ skinny A@Bᵀ
 // Decode-shaped C[M ≤ 16·MT, N] = X[M, K]·W[N, K]ᵀ (M = sequences decoded
 // together): bound by streaming W once, and too small for the tiled
@@ -920,6 +938,11 @@ static int partials(aur_ctx* ctx, const Workspace* ws, size_t floats, float** ou
 static void reduce_partials(aur_ctx* ctx, const float* P, float* C, int M, int N, int ldc, int splits,
                             const Epilogue& epi) {
   const size_t total = (size_t)M * N;
+  if (N % 4 == 0 && total < (size_t(1) << 32) && splits > 0 && aligned16(P)) {
+    const int blocks = (int)std::min<size_t>((total / 4 + 255) / 256, 4096);
+    hipLaunchKernelGGL(splitk_reduce4, dim3(blocks), dim3(256), 0, ctx->stream, P, C, M, N, ldc, splits, epi);
+    return;
+  }
   int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, P, C, M, N, ldc, splits, epi);
 }
