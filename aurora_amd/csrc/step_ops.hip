@@ -379,36 +379,144 @@ __global__ void __launch_bounds__(256) ln_param_partial_kernel(const float* __re
   pb[(size_t)chunk * d + c] = sb;
 }
 
+// ln_bwd_vec_kernel fused with the γ/β partial sums, so that x and dy are read
+// once for dx, dγ and dβ.  A block owns LN_FCHUNK consecutive rows, eight per
+// wave; each lane keeps Σ dy·x̂ and Σ dy for its columns over its wave's rows
+// (ascending r), the four waves' sums are added in wave order through LDS, and
+// wave 0 writes the chunk's partial row of pg / pb.  For NV ≤ 4 the loads of
+// two rows are issued before either is reduced, to keep more bytes in flight.
+constexpr int LN_FCHUNK = 32;
+template <int NV>
+__global__ void __launch_bounds__(256) ln_bwd_fused_kernel(const float* __restrict__ x,
+                                                           const float* __restrict__ mean,
+                                                           const float* __restrict__ rstd,
+                                                           const float* __restrict__ gamma,
+                                                           const float* __restrict__ dy,
+                                                           const float* __restrict__ dres,
+                                                           float* __restrict__ dx, float* __restrict__ pg,
+                                                           float* __restrict__ pb, int rows) {
+  constexpr int D = 256 * NV;
+  constexpr int RPW = LN_FCHUNK / 4;
+  constexpr int RB = NV <= 4 ? 2 : 1;
+  __shared__ floatx4 red[2][3][64 * NV];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rbase = blockIdx.x * LN_FCHUNK + w * RPW;
+  const floatx4* g4 = reinterpret_cast<const floatx4*>(gamma);
+  floatx4 gam[NV], accg[NV], accb[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    gam[i] = g4[lane + 64 * i];
+    accg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    accb[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float inv_d = 1.0f / (float)D;
+  for (int j = 0; j < RPW; j += RB) {
+    floatx4 xv[RB][NV], dv[RB][NV];
+    float mu[RB], s[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      // A row past the end is clamped to the last row: its loads stay in
+      // bounds and its results are never used.
+      const int rr = min(rbase + j + b, rows - 1);
+      mu[b] = mean[rr];
+      s[b] = rstd[rr];
+      const floatx4* xr = reinterpret_cast<const floatx4*>(x + (size_t)rr * D);
+      const floatx4* dyr = reinterpret_cast<const floatx4*>(dy + (size_t)rr * D);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        xv[b][i] = xr[lane + 64 * i];
+        dv[b][i] = dyr[lane + 64 * i];
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      const int r = rbase + j + b;
+      if (r >= rows) break;  // r depends only on the wave: uniform
+      floatx4 g[NV], xh[NV];
+      float sg = 0.f, sgx = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          g[i][e] = dv[b][i][e] * gam[i][e];
+          xh[i][e] = (xv[b][i][e] - mu[b]) * s[b];
+          sg += g[i][e];
+          sgx += g[i][e] * xh[i][e];
+          accg[i][e] += dv[b][i][e] * xh[i][e];
+          accb[i][e] += dv[b][i][e];
+        }
+      }
+      sg = wave_sum(sg);
+      sgx = wave_sum(sgx);
+      floatx4* dxr = reinterpret_cast<floatx4*>(dx + (size_t)r * D);
+      const floatx4* dr = dres ? reinterpret_cast<const floatx4*>(dres + (size_t)r * D) : nullptr;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        floatx4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = s[b] * (g[i][e] - inv_d * (sg + xh[i][e] * sgx));
+        if (dr) o += dr[lane + 64 * i];
+        dxr[lane + 64 * i] = o;
+      }
+    }
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      red[0][w - 1][lane + 64 * i] = accg[i];
+      red[1][w - 1][lane + 64 * i] = accb[i];
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    floatx4* pgr = reinterpret_cast<floatx4*>(pg + (size_t)blockIdx.x * D);
+    floatx4* pbr = reinterpret_cast<floatx4*>(pb + (size_t)blockIdx.x * D);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      floatx4 sgv = accg[i], sbv = accb[i];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        sgv += red[0][k][lane + 64 * i];
+        sbv += red[1][k][lane + 64 * i];
+      }
+      pgr[lane + 64 * i] = sgv;
+      pbr[lane + 64 * i] = sbv;
+    }
+  }
+}
+
 // dγ[c] += Σ_chunk pg[chunk][c], dβ[c] += Σ_chunk pb[chunk][c].  A block owns
-// 16 columns; its 256 threads are 16 columns × 16 chunk classes (chunk ≡ q
-// mod 16, summed ascending), and the 16 class sums are added in class order
-// through LDS — a fixed order, so the result is deterministic, with 16× the
-// parallelism of one thread per column.
+// 4 columns; its 256 threads are 4 columns × 64 chunk classes (thread
+// q·4 + col takes chunks ≡ q mod 64, summed ascending).  A wave's 16 class
+// sums per column are combined by a fixed xor butterfly and the four waves'
+// sums are added in wave order through LDS — a fixed order, so the result is
+// deterministic — with d / 4 blocks to spread the partial rows' reads.
 __global__ void __launch_bounds__(256) ln_param_final_kernel(const float* __restrict__ pg,
                                                              const float* __restrict__ pb,
                                                              int nchunks, float* __restrict__ dgamma,
                                                              float* __restrict__ dbeta, int d) {
-  __shared__ float sg_[16][17], sb_[16][17];
-  const int col = threadIdx.x & 15, q = threadIdx.x >> 4;
-  const int c = blockIdx.x * 16 + col;
+  __shared__ float sg_[4][4], sb_[4][4];
+  const int col = threadIdx.x & 3, q = threadIdx.x >> 2, w = threadIdx.x >> 6;
+  const int c = blockIdx.x * 4 + col;
   float sg = 0.f, sb = 0.f;
   if (c < d)
-    for (int k = q; k < nchunks; k += 16) {
+    for (int k = q; k < nchunks; k += 64) {
       sg += pg[(size_t)k * d + c];
       sb += pb[(size_t)k * d + c];
     }
-  sg_[q][col] = sg;
-  sb_[q][col] = sb;
-  __syncthreads();
-  if (q == 0 && c < d) {
-    float tg = 0.f, tb = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      tg += sg_[i][col];
-      tb += sb_[i][col];
-    }
-    dgamma[c] += tg;
-    dbeta[c] += tb;
+  for (int m = 4; m < 64; m <<= 1) {
+    sg += __shfl_xor(sg, m, 64);
+    sb += __shfl_xor(sb, m, 64);
+  }
+  if ((threadIdx.x & 63) < 4) {
+    sg_[w][col] = sg;
+    sb_[w][col] = sb;
+  }
+  __syncthreads();
+  if (threadIdx.x < 4 && c < d) {
+    dgamma[c] += ((sg_[0][col] + sg_[1][col]) + sg_[2][col]) + sg_[3][col];
+    dbeta[c] += ((sb_[0][col] + sb_[1][col]) + sb_[2][col]) + sb_[3][col];
   }
 }
 
@@ -747,7 +855,8 @@ int layer_norm_forward_sum(aur_ctx* ctx, const float* R, const float* P, int np,
 }
 
 size_t layer_norm_backward_ws_floats(int rows, int d) {
-  return 2 * (size_t)((rows + LN_CHUNK - 1) / LN_CHUNK) * d;
+  static_assert(LN_FCHUNK <= LN_CHUNK, "the fused kernel's chunks are the finer ones");
+  return 2 * (size_t)((rows + LN_FCHUNK - 1) / LN_FCHUNK) * d;
 }
 
 int layer_norm_backward(aur_ctx* ctx, const float* x, const float* mean, const float* rstd,
@@ -756,6 +865,25 @@ int layer_norm_backward(aur_ctx* ctx, const float* x, const float* mean, const f
   const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma) |
                      reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(dres) |
                      reinterpret_cast<uintptr_t>(dx)) & 15) == 0;
+  const bool fused = vec && (reinterpret_cast<uintptr_t>(ws) & 15) == 0 && rows > 0 &&
+                     (d == 256 || d == 512 || d == 1024 || d == 2048) && getenv("AUR_LN_UNFUSED") == nullptr;
+  if (fused) {
+    const int nch = (rows + LN_FCHUNK - 1) / LN_FCHUNK;
+    float* pg = ws;
+    float* pb = ws + (size_t)nch * d;
+    const dim3 gc(nch);
+    if (d == 256)
+      hipLaunchKernelGGL(ln_bwd_fused_kernel<1>, gc, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, pg, pb, rows);
+    else if (d == 512)
+      hipLaunchKernelGGL(ln_bwd_fused_kernel<2>, gc, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, pg, pb, rows);
+    else if (d == 1024)
+      hipLaunchKernelGGL(ln_bwd_fused_kernel<4>, gc, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, pg, pb, rows);
+    else
+      hipLaunchKernelGGL(ln_bwd_fused_kernel<8>, gc, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, pg, pb, rows);
+    hipLaunchKernelGGL(ln_param_final_kernel, dim3((d + 3) / 4), dim3(256), 0, ctx->stream, pg, pb, nch,
+                       dgamma, dbeta, d);
+    LAUNCH_OK(ctx, "ln_bwd_fused kernels");
+  }
   const dim3 g4((rows + 3) / 4);
   if (vec && d == 256)
     hipLaunchKernelGGL(ln_bwd_vec_kernel<1>, g4, dim3(256), 0, ctx->stream, x, mean, rstd, gamma, dy, dres, dx, rows);
@@ -772,7 +900,7 @@ int layer_norm_backward(aur_ctx* ctx, const float* x, const float* mean, const f
   float* pb = ws + (size_t)nch * d;
   hipLaunchKernelGGL(ln_param_partial_kernel, dim3((d + 255) / 256, nch), dim3(256), 0, ctx->stream, x,
                      mean, rstd, dy, pg, pb, rows, d);
-  hipLaunchKernelGGL(ln_param_final_kernel, dim3((d + 15) / 16), dim3(256), 0, ctx->stream, pg, pb, nch,
+  hipLaunchKernelGGL(ln_param_final_kernel, dim3((d + 3) / 4), dim3(256), 0, ctx->stream, pg, pb, nch,
                      dgamma, dbeta, d);
   LAUNCH_OK(ctx, "ln_bwd kernels");
 }

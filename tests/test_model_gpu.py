@@ -96,20 +96,47 @@ def test_config0_train_step_matches_cpu(ctx):
     m.destroy()
 
 
-def test_train_step_wide_rows_matches_cpu(ctx):
-    """d_model 256 over B·T = 1024 rows: the row-resident float4 LayerNorm
-    forward / backward paths (d = 256·k, ≥ 1024 rows) against the oracle."""
-    cfg = OM.Config(vocab=128, d_model=256, n_layer=1, n_head=4, d_ff=512, seq_len_max=256)
+@pytest.mark.parametrize("d,B,T", [(256, 4, 256), (512, 3, 200)])
+def test_train_step_wide_rows_matches_cpu(ctx, d, B, T):
+    """d_model 256 / 512 over B·T = 1024 / 600 rows: the row-resident float4
+    LayerNorm forward and the fused LayerNorm backward (dx with the γ/β chunk
+    partials; 600 rows leave a partial last chunk of 32 rows) against the
+    oracle."""
+    cfg = OM.Config(vocab=128, d_model=d, n_layer=1, n_head=d // 64, d_ff=2 * d, seq_len_max=256)
     P = OM.init_params(cfg, 5)
-    tok, tgt = _tokens(cfg, 4, 256, 5)
-    m = _gpu_model(ctx, cfg, 4, P)
+    tok, tgt = _tokens(cfg, B, T, 5)
+    m = _gpu_model(ctx, cfg, B, P)
     m.zero_grad()
     loss_gpu = m.train_step_batch(tok, tgt)
     loss_cpu, G = OM.batch_grads(P, cfg, tok, tgt)
-    assert abs(loss_gpu - loss_cpu) < 5e-3 * 4, (loss_gpu, loss_cpu)
+    assert abs(loss_gpu - loss_cpu) < 5e-3 * B, (loss_gpu, loss_cpu)
     worst = _compare_tree(m.read_tensors(grad=True), G, 1e-3, "grad")
-    print(f"[d256] loss gpu {loss_gpu:.6f} cpu {loss_cpu:.6f} |grad err| <= {worst:.2e}")
+    print(f"[d{d} rows {B * T}] loss gpu {loss_gpu:.6f} cpu {loss_cpu:.6f} |grad err| <= {worst:.2e}")
     m.destroy()
+
+
+def test_fused_layernorm_backward_equals_unfused(ctx, monkeypatch):
+    """d_model 1024 over 2 × 100 rows (seven 32-row chunks, the last one
+    partial): the fused LayerNorm backward gives the gradients of the
+    separate dx / γ-β partial kernels (AUR_LN_UNFUSED); dx is computed
+    identically, dγ / dβ differ only in summation order."""
+    cfg = OM.Config(vocab=64, d_model=1024, n_layer=1, n_head=16, d_ff=1024, seq_len_max=128)
+    P = OM.init_params(cfg, 9)
+    tok, tgt = _tokens(cfg, 2, 100, 9)
+    grads = []
+    for unfused in (False, True):
+        if unfused:
+            monkeypatch.setenv("AUR_LN_UNFUSED", "1")
+        m = _gpu_model(ctx, cfg, 2, P)
+        m.zero_grad()
+        m.train_step_batch(tok, tgt)
+        grads.append(m.read_tensors(grad=True))
+        m.destroy()
+    monkeypatch.delenv("AUR_LN_UNFUSED")
+    for (name, l, a), (_, _, b) in zip(OM.tensors(grads[0]), OM.tensors(grads[1])):
+        a, b = np.asarray(a), np.asarray(b)
+        scale = max(1e-6, float(np.abs(b).max()))
+        assert float(np.abs(a - b).max()) <= 1e-5 * scale, (name, l)
 
 
 def test_fused_clip_adamw_equals_separate(ctx):
