@@ -411,7 +411,7 @@ __global__ void __launch_bounds__(256) ln_bwd_fused_kernel(const float* __restri
   }
   const float inv_d = 1.0f / (float)D;
   for (int j = 0; j < RPW; j += RB) {
-    floatx4 xv[RB][NV], dv[RB][NV];
+    floatx4 xv[RB][NV], dv[RB][NV], rv[RB][NV];
     float mu[RB], s[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
@@ -426,6 +426,16 @@ __global__ void __launch_bounds__(256) ln_bwd_fused_kernel(const float* __restri
       for (int i = 0; i < NV; ++i) {
         xv[b][i] = xr[lane + 64 * i];
         dv[b][i] = dyr[lane + 64 * i];
+      }
+      // The residual gradient is loaded with x and dy, not after the row's
+      // reductions, so its latency overlaps theirs.
+      if (dres) {
+        const floatx4* drr = reinterpret_cast<const floatx4*>(dres + (size_t)rr * D);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) rv[b][i] = drr[lane + 64 * i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) rv[b][i] = floatx4{0.f, 0.f, 0.f, 0.f};
       }
     }
 #pragma unroll
@@ -449,13 +459,12 @@ __global__ void __launch_bounds__(256) ln_bwd_fused_kernel(const float* __restri
       sg = wave_sum(sg);
       sgx = wave_sum(sgx);
       floatx4* dxr = reinterpret_cast<floatx4*>(dx + (size_t)r * D);
-      const floatx4* dr = dres ? reinterpret_cast<const floatx4*>(dres + (size_t)r * D) : nullptr;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         floatx4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = s[b] * (g[i][e] - inv_d * (sg + xh[i][e] * sgx));
-        if (dr) o += dr[lane + 64 * i];
+        if (dres) o += rv[b][i];
         dxr[lane + 64 * i] = o;
       }
     }
