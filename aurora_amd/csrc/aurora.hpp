@@ -195,11 +195,16 @@ struct CheckpointHeader {
 CheckpointHeader read_checkpoint_header(const char* path);
 CheckpointHeader read_checkpoint_header(std::FILE* f);
 
+// How train_step_batch combines the B per-sequence gradients (each of a
+// mean-over-T cross-entropy): Sum is the reference GPU model's convention
+// (src/gpu/transformer.rs:1555-1559; its trainer scales the clip threshold by
+// B, examples/aurora_train.rs:1046-1051), Mean the CPU trainer's
+// grads.scale(1/B) (examples/aurora_train.rs:840-846).
+enum class BatchReduction : uint32_t { Mean = AUR_BATCH_MEAN, Sum = AUR_BATCH_SUM };
+
 // The reference's DecoderTransformerGpu at M = B·T rows: B sequences of
 // length T run through every GEMM together (the reference serialises them,
-// one sequence per GEMM).  Gradient convention: per-sequence mean-over-T
-// cross-entropy, averaged over the batch (the CPU trainer's grads.scale(1/B),
-// examples/aurora_train.rs:840-846).
+// one sequence per GEMM).
 class DecoderTransformerGpu {
  public:
   DecoderTransformerGpu(aur_ctx* ctx, const TransformerConfig& cfg, uint32_t max_batch);
@@ -219,8 +224,10 @@ class DecoderTransformerGpu {
 
   void zero_grad();
   // Forward + softmax-CE + backward for b sequences of length t; gradients
-  // accumulate.  Returns Σ_b mean_t NLL_b (src/gpu/transformer.rs:1571-1615).
-  float train_step_batch(const uint32_t* tokens, const uint32_t* targets, uint32_t b, uint32_t t);
+  // accumulate, combined over the batch as `red` says.  Returns
+  // Σ_b mean_t NLL_b (src/gpu/transformer.rs:1571-1615).
+  float train_step_batch(const uint32_t* tokens, const uint32_t* targets, uint32_t b, uint32_t t,
+                         BatchReduction red = BatchReduction::Mean);
   // Forward only; logits [b·t, vocab] to the host if non-null.
   void forward(const uint32_t* tokens, uint32_t b, uint32_t t, float* logits_host);
   // Forward + softmax-CE with loss scale 1 and no backward: per-token NLL in
@@ -229,13 +236,16 @@ class DecoderTransformerGpu {
   // (src/gpu/transformer.rs:1723-1811).
   void eval_step_batch(const uint32_t* tokens, const uint32_t* targets, uint32_t b, uint32_t t,
                        float* nll_host);
+  // grad_norm (src/gpu/transformer.rs:1263): global L2 norm over all grads.
+  float grad_norm();
   // model.rs:1011-1017: global L2 norm over all grads, scaled in place when
-  // above max_norm; returns the pre-clip norm.
-  float clip_grads(float max_norm);
+  // above max_norm; returns the pre-clip norm, or NaN without the host read
+  // when want_norm is false (src/gpu/transformer.rs:2294 want_norm).
+  float clip_grads(float max_norm, bool want_norm = true);
   // model.rs:926-1009 (decay on w_tok, Q/K/V/O, fc, proj; none on LN, w_pos).
   void step_adamw(const AdamWConfig& cfg);
   // clip_grads + step_adamw without the separate scaling pass.
-  float clip_and_step_adamw(float max_norm, const AdamWConfig& cfg);
+  float clip_and_step_adamw(float max_norm, const AdamWConfig& cfg, bool want_norm = true);
 
   // Muon hybrid (model.rs:1023-1090, gpu/transformer.rs:2052-2291): AdamW on
   // the embeddings and LayerNorm γ/β, Muon (momentum → Frobenius bound →
@@ -244,8 +254,18 @@ class DecoderTransformerGpu {
   // first call.
   void step_muon_hybrid(const MuonConfig& muon, const AdamWConfig& adam);
   // model.rs:1101-1107: L2 norm over the AdamW subset only, which is scaled
-  // to max_norm when above it; returns the pre-clip norm.
-  float clip_grads_adamw_subset(float max_norm);
+  // to max_norm when above it; returns the pre-clip norm (NaN when
+  // want_norm is false: no host read).
+  float clip_grads_adamw_subset(float max_norm, bool want_norm = true);
+
+  // snapshot_state / refresh_state / restore_state (src/gpu/transformer.rs:
+  // 1152-1240): the persistent state — parameters, both AdamW moments and,
+  // once allocated, the Muon momentum — as one device-to-device copy into or
+  // out of a caller-owned buffer of state_bytes() bytes.  The optimizer step
+  // counter travels separately (`step`).
+  size_t state_bytes() const;
+  void copy_state_to(void* dst) const;
+  void copy_state_from(const void* src);
 
   // Zero the optimizer state (AdamW moments, Muon momentum) — a fresh optimizer.
   void reset_optimizer_state();
@@ -255,7 +275,9 @@ class DecoderTransformerGpu {
   void save_checkpoint(const char* path, uint32_t epoch, uint64_t step) const;
   CheckpointHeader load_checkpoint(const char* path);
 
-  // KV decode (src/gpu/transformer.rs:2374-2640, batched).
+  // KV decode (src/gpu/transformer.rs:2374-2640, batched).  A cache serves
+  // only the model it was created from (its captured decode step holds that
+  // model's weight pointers); other models get AUR_EINVAL.
   void prefill_kv(KvCacheGpu& cache, const uint32_t* tokens, uint32_t b, uint32_t t, float* last_logits);
   void generate_step_kv(KvCacheGpu& cache, const uint32_t* tokens, float* logits_host,
                         uint32_t* next_tokens_host);
@@ -269,6 +291,7 @@ class DecoderTransformerGpu {
   void ensure_decode_graph(KvCacheGpu& cache);
   void encode_backward(uint32_t b, uint32_t t);
   void upload_tokens(const uint32_t* tokens, const uint32_t* targets, uint32_t b, uint32_t t);
+  void check_cache(const KvCacheGpu& cache) const;
 
   aur_ctx* ctx_;
   TransformerConfig cfg_;
@@ -283,14 +306,19 @@ class DecoderTransformerGpu {
   float *params_ = nullptr, *grads_ = nullptr, *m1_ = nullptr, *m2_ = nullptr;
   std::vector<Layer>* layers_ = nullptr;
   Acts* acts_ = nullptr;
+  // Live caches created from this model; on destruction they are detached
+  // (their decode graphs, which read this model's weights, are dropped).
+  std::vector<KvCacheGpu*> caches_;
 };
 
 // Per-layer K/V history for a batch of sequences decoded together:
 // [n_layer][batch][max_len][d_model] each for K and V, plus the device-side
-// positions and decode activations (src/gpu/kv_cache.rs:21-92).
+// positions and decode activations (src/gpu/kv_cache.rs:21-92).  It belongs
+// to the model it is created from and must not outlive it in use: once that
+// model is destroyed the cache can only be destroyed.
 class KvCacheGpu {
  public:
-  KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch, uint32_t max_len);
+  KvCacheGpu(DecoderTransformerGpu& model, uint32_t batch, uint32_t max_len);
   ~KvCacheGpu();
   KvCacheGpu(const KvCacheGpu&) = delete;
   KvCacheGpu& operator=(const KvCacheGpu&) = delete;
@@ -303,7 +331,9 @@ class KvCacheGpu {
 
  private:
   friend class DecoderTransformerGpu;
+  void drop_graph();
   aur_ctx* ctx_;
+  DecoderTransformerGpu* owner_;  // nullptr once the model is destroyed
   void* mem_ = nullptr;
   float *k_ = nullptr, *v_ = nullptr;
   int32_t *pos_ = nullptr, *lens_ = nullptr;

@@ -30,6 +30,15 @@ int set_error(aur_ctx* ctx, int code, const char* fmt, ...) {
 
 int ensure_workspace(aur_ctx* ctx, size_t bytes) {
   if (bytes <= ctx->ws_bytes) return 0;
+  // Growing the workspace synchronises the stream and frees / allocates
+  // memory, none of which may happen while the stream is being captured
+  // into a HIP graph (the graph would also keep the old pointer).  Work that
+  // is captured passes its own Workspace instead.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  AUR_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return set_error(ctx, AUR_EINVAL,
+                     "workspace of %zu bytes needed while the stream is captured; pass a Workspace", bytes);
   if (ctx->ws) {
     // The old workspace may still be read by enqueued kernels.
     AUR_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -43,13 +52,8 @@ int ensure_workspace(aur_ctx* ctx, size_t bytes) {
   if (e != hipSuccess)
     return set_error(ctx, AUR_ENOMEM, "workspace of %zu bytes: %s", want,
                      hipGetErrorString(e));
-  // Zeroed once: the head of the workspace holds arrival counters that every
-  // kernel using them leaves at zero when it finishes.
-  e = hipMemsetAsync(p, 0, want, ctx->stream);
-  if (e != hipSuccess) {
-    hipFree(p);
-    return set_error(ctx, (int)e, "workspace memset: %s", hipGetErrorString(e));
-  }
+  // No clearing: every user (split-K partial tiles) writes the region it
+  // reads back before reading it.
   ctx->ws = p;
   ctx->ws_bytes = want;
   return 0;

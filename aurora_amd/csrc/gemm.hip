@@ -1119,6 +1119,12 @@ int gemm_nt_partials_splits(int M, int N, int K) {
   const int groups = (N + 63) / 64;
   int s = 1;
   while (groups * s < 256 && K / (2 * s) >= 64) s *= 2;
+  // gemm_nt_partials cuts K into ranges of a multiple of 64: keep only a
+  // count whose ranges are all non-empty (K = 384 fits 3 ranges of 128, not 4).
+  for (; s > 1; --s) {
+    const int chunk = ((K + s - 1) / s + 63) / 64 * 64;
+    if ((K + chunk - 1) / chunk == s) break;
+  }
   return s;
 }
 

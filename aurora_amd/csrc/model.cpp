@@ -226,6 +226,10 @@ DecoderTransformerGpu::DecoderTransformerGpu(aur_ctx* ctx, const TransformerConf
 }
 
 DecoderTransformerGpu::~DecoderTransformerGpu() {
+  for (KvCacheGpu* c : caches_) {
+    c->drop_graph();
+    c->owner_ = nullptr;
+  }
   if (ctx_) {
     aur_sync(ctx_);
     if (acts_ && acts_->pin) (void)hipHostFree(acts_->pin);
@@ -379,7 +383,7 @@ void DecoderTransformerGpu::encode_backward(uint32_t b, uint32_t t) {
 }
 
 float DecoderTransformerGpu::train_step_batch(const uint32_t* tokens, const uint32_t* targets, uint32_t b,
-                                              uint32_t t) {
+                                              uint32_t t, BatchReduction red) {
   if (b == 0 || t == 0) return 0.f;
   if (b > max_batch_ || t > cfg_.seq_len_max) throw Error("train_step_batch: batch/seq too large", AUR_ELIMIT);
   auto& A = *acts_;
@@ -418,9 +422,10 @@ float DecoderTransformerGpu::train_step_batch(const uint32_t* tokens, const uint
   up(A.csr_idx, A.pin_csr_idx, M * 4, "csr idx");
   hip_ck(ctx_, hipEventRecord(A.pin_done, st), "train_step_batch: staging event");
 
-  // CE with 1/T per sequence and the batch mean folded into one scale.
-  ck(ctx_, aur::softmax_ce(ctx_, A.logits, A.tgt, A.nll, (int)M, (int)cfg_.vocab, 1.0f / ((float)t * b)),
-     "softmax_ce");
+  // CE with 1/T per sequence (model.rs:820-858), and for the batch mean the
+  // 1/B folded into the same scale; the sum convention keeps 1/T alone.
+  const float ce_scale = red == BatchReduction::Sum ? 1.0f / (float)t : 1.0f / ((float)t * b);
+  ck(ctx_, aur::softmax_ce(ctx_, A.logits, A.tgt, A.nll, (int)M, (int)cfg_.vocab, ce_scale), "softmax_ce");
   encode_backward(b, t);
   ck(ctx_, aur::embed_backward(ctx_, A.dx_a, (int)b, (int)t, (int)cfg_.d_model, A.csr_tok, A.csr_off, A.csr_idx,
                                (int)nuniq, A.g_w_tok, A.g_w_pos),
@@ -455,10 +460,19 @@ void DecoderTransformerGpu::eval_step_batch(const uint32_t* tokens, const uint32
   ck(ctx_, aur_d2h(ctx_, nll_host, A.nll, M * 4), "download nll");
 }
 
-float DecoderTransformerGpu::clip_grads(float max_norm) {
+float DecoderTransformerGpu::grad_norm() {
+  auto& A = *acts_;
+  ck(ctx_, aur::grad_norm(ctx_, grads_, n_params_, INFINITY, A.norm_part, A.stats), "grad norm");
+  float nrm = 0.f;
+  ck(ctx_, aur_d2h(ctx_, &nrm, A.stats, 4), "download norm");
+  return nrm;
+}
+
+float DecoderTransformerGpu::clip_grads(float max_norm, bool want_norm) {
   auto& A = *acts_;
   ck(ctx_, aur::grad_norm(ctx_, grads_, n_params_, max_norm, A.norm_part, A.stats), "grad norm");
   ck(ctx_, aur::scale_by(ctx_, grads_, n_params_, A.stats + 1), "clip scale");
+  if (!want_norm) return NAN;
   float nrm = 0.f;
   ck(ctx_, aur_d2h(ctx_, &nrm, A.stats, 4), "download norm");
   return nrm;
@@ -484,13 +498,14 @@ void DecoderTransformerGpu::reset_optimizer_state() {
 // w_fc, w_proj) occupy [V·d, n_decay) of the flat buffers; the Muon momentum
 // buffer mirrors that region.  Newton–Schulz scratch is sized for the
 // largest matrix: m = min(rows, cols) = d for every one, n = max ≤ d_ff.
-float DecoderTransformerGpu::clip_grads_adamw_subset(float max_norm) {
+float DecoderTransformerGpu::clip_grads_adamw_subset(float max_norm, bool want_norm) {
   auto& A = *acts_;
   const size_t n_tok = (size_t)cfg_.vocab * cfg_.d_model, n_rest = n_params_ - n_decay_;
   ck(ctx_, aur::grad_norm2(ctx_, grads_, n_tok, grads_ + n_decay_, n_rest, max_norm, A.norm_part, A.stats),
      "subset norm");
   ck(ctx_, aur::scale_by(ctx_, grads_, n_tok, A.stats + 1), "subset clip");
   ck(ctx_, aur::scale_by(ctx_, grads_ + n_decay_, n_rest, A.stats + 1), "subset clip");
+  if (!want_norm) return NAN;
   float nrm = 0.f;
   ck(ctx_, aur_d2h(ctx_, &nrm, A.stats, 4), "download norm");
   return nrm;
@@ -611,7 +626,7 @@ void DecoderTransformerGpu::step_adamw(const AdamWConfig& c) {
      "adamw");
 }
 
-float DecoderTransformerGpu::clip_and_step_adamw(float max_norm, const AdamWConfig& c) {
+float DecoderTransformerGpu::clip_and_step_adamw(float max_norm, const AdamWConfig& c, bool want_norm) {
   auto& A = *acts_;
   ck(ctx_, aur::grad_norm(ctx_, grads_, n_params_, max_norm, A.norm_part, A.stats), "grad norm");
   step += 1;
@@ -619,16 +634,44 @@ float DecoderTransformerGpu::clip_and_step_adamw(float max_norm, const AdamWConf
   ck(ctx_, aur::adamw(ctx_, params_, grads_, m1_, m2_, n_params_, n_decay_, A.stats + 1, c.lr, c.beta1,
                       c.beta2, c.eps, c.weight_decay, bc1, bc2),
      "adamw");
+  if (!want_norm) return NAN;
   float nrm = 0.f;
   ck(ctx_, aur_d2h(ctx_, &nrm, A.stats, 4), "download norm");
   return nrm;
 }
 
+// ------------------------------------------------------------ state snapshot
+// params | m1 | m2 are contiguous thirds of state_mem_ apart from grads, so
+// the copy is three device-to-device copies, plus the Muon momentum.
+size_t DecoderTransformerGpu::state_bytes() const {
+  const size_t mom = mu_ ? (n_decay_ - (size_t)cfg_.vocab * cfg_.d_model) : 0;
+  return (3 * n_params_ + mom) * sizeof(float);
+}
+
+void DecoderTransformerGpu::copy_state_to(void* dst) const {
+  if (!dst) throw Error("copy_state_to: null buffer", AUR_EINVAL);
+  float* d = static_cast<float*>(dst);
+  const size_t n = n_params_ * sizeof(float);
+  ck(ctx_, aur_d2d(ctx_, d, params_, n), "snapshot params");
+  ck(ctx_, aur_d2d(ctx_, d + n_params_, m1_, 2 * n), "snapshot moments");
+  if (mu_)
+    ck(ctx_, aur_d2d(ctx_, d + 3 * n_params_, mu_, state_bytes() - 3 * n), "snapshot muon momentum");
+}
+
+void DecoderTransformerGpu::copy_state_from(const void* src) {
+  if (!src) throw Error("copy_state_from: null buffer", AUR_EINVAL);
+  const float* s = static_cast<const float*>(src);
+  const size_t n = n_params_ * sizeof(float);
+  ck(ctx_, aur_d2d(ctx_, params_, s, n), "restore params");
+  ck(ctx_, aur_d2d(ctx_, m1_, s + n_params_, 2 * n), "restore moments");
+  if (mu_) ck(ctx_, aur_d2d(ctx_, mu_, s + 3 * n_params_, state_bytes() - 3 * n), "restore muon momentum");
+}
+
 // ------------------------------------------------------------------ KV cache
 
-KvCacheGpu::KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch_, uint32_t max_len_)
+KvCacheGpu::KvCacheGpu(DecoderTransformerGpu& model, uint32_t batch_, uint32_t max_len_)
     : batch(batch_), max_len(max_len_), d_model(model.config().d_model), n_layer(model.config().n_layer),
-      ctx_(model.ctx()) {
+      ctx_(model.ctx()), owner_(&model) {
   const auto& c = model.config();
   if (batch == 0 || max_len == 0 || max_len > c.seq_len_max)
     throw Error("KvCacheGpu: batch > 0 and 0 < max_len <= seq_len_max required", AUR_EINVAL);
@@ -663,12 +706,28 @@ KvCacheGpu::KvCacheGpu(const DecoderTransformerGpu& model, uint32_t batch_, uint
   pos_ = cv.take<int32_t>(B);
   lens_ = cv.take<int32_t>(B);
   tok_ = cv.take<uint32_t>(B);
-  if (cv.off > bytes_) throw Error("KvCacheGpu: arena overflow", AUR_ENOMEM);
+  if (cv.off > bytes_) {
+    aur_free(ctx_, mem_);
+    throw Error("KvCacheGpu: arena overflow", AUR_ENOMEM);
+  }
   reset();
+  model.caches_.push_back(this);
+}
+
+void KvCacheGpu::drop_graph() {
+  if (graph_) {
+    aur_sync(ctx_);  // a replay may still be running
+    hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_));
+    graph_ = nullptr;
+  }
 }
 
 KvCacheGpu::~KvCacheGpu() {
-  if (graph_) hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_));
+  if (owner_) {
+    auto& v = owner_->caches_;
+    v.erase(std::remove(v.begin(), v.end(), this), v.end());
+  }
+  drop_graph();
   if (mem_) aur_free(ctx_, mem_);
 }
 
@@ -677,8 +736,15 @@ void KvCacheGpu::reset() {
   current_len = 0;
 }
 
+void DecoderTransformerGpu::check_cache(const KvCacheGpu& cache) const {
+  if (cache.owner_ != this)
+    throw Error(cache.owner_ ? "KV cache belongs to another model" : "KV cache's model was destroyed",
+                AUR_EINVAL);
+}
+
 void DecoderTransformerGpu::prefill_kv(KvCacheGpu& cache, const uint32_t* tokens, uint32_t b, uint32_t t,
                                        float* last_logits) {
+  check_cache(cache);
   if (b != cache.batch) throw Error("prefill_kv: batch differs from the cache's", AUR_EINVAL);
   if (t == 0 || t > cache.max_len || b > max_batch_) throw Error("prefill_kv: bad length", AUR_EINVAL);
   cache.reset();
@@ -725,6 +791,7 @@ void DecoderTransformerGpu::ensure_decode_graph(KvCacheGpu& cache) {
 
 void DecoderTransformerGpu::generate_step_kv(KvCacheGpu& cache, const uint32_t* tokens, float* logits_host,
                                              uint32_t* next_tokens_host) {
+  check_cache(cache);
   if (cache.current_len >= cache.max_len) throw Error("generate_step_kv: cache full", AUR_ELIMIT);
   const int B = (int)cache.batch, V = (int)cfg_.vocab;
   if (tokens) {
@@ -843,7 +910,7 @@ struct aur_model {
 };
 struct aur_kv_cache {
   KvCacheGpu* c;
-  aur_model* owner;
+  aur_ctx* ctx;  // the context of the model it was created from (which may be gone)
 };
 
 namespace {
@@ -917,7 +984,7 @@ int aur_model_step_muon_hybrid(aur_model* m, float muon_lr, float momentum, int3
 int aur_model_clip_grads_adamw_subset(aur_model* m, float max_norm, float* norm) {
   if (!m) return AUR_EINVAL;
   return guard(m->m->ctx(), [&] {
-    const float n = m->m->clip_grads_adamw_subset(max_norm);
+    const float n = m->m->clip_grads_adamw_subset(max_norm, norm != nullptr);
     if (norm) *norm = n;
   });
 }
@@ -950,10 +1017,44 @@ int aur_model_save_checkpoint(aur_model* m, const char* path, uint32_t epoch, ui
 
 int aur_model_train_step_batch(aur_model* m, const uint32_t* tokens, const uint32_t* targets, uint32_t b,
                                uint32_t t, float* loss_sum) {
+  return aur_model_train_step_batch_ex(m, tokens, targets, b, t, AUR_BATCH_MEAN, loss_sum);
+}
+
+int aur_model_train_step_batch_ex(aur_model* m, const uint32_t* tokens, const uint32_t* targets, uint32_t b,
+                                  uint32_t t, uint32_t reduction, float* loss_sum) {
   if (!m || !tokens || !targets) return AUR_EINVAL;
+  if (reduction != AUR_BATCH_MEAN && reduction != AUR_BATCH_SUM)
+    return aur::set_error(m->m->ctx(), AUR_EINVAL, "aur_model_train_step_batch_ex: reduction %u", reduction);
   return guard(m->m->ctx(), [&] {
-    float l = m->m->train_step_batch(tokens, targets, b, t);
+    float l = m->m->train_step_batch(tokens, targets, b, t, static_cast<aurora::BatchReduction>(reduction));
     if (loss_sum) *loss_sum = l;
+  });
+}
+
+int aur_model_grad_norm(aur_model* m, float* norm) {
+  if (!m || !norm) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] { *norm = m->m->grad_norm(); });
+}
+
+int aur_model_state_bytes(aur_model* m, size_t* bytes) {
+  if (!m || !bytes) return AUR_EINVAL;
+  *bytes = m->m->state_bytes();
+  return 0;
+}
+
+int aur_model_state_save(aur_model* m, void* dst, uint64_t* step) {
+  if (!m || !dst) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] {
+    m->m->copy_state_to(dst);
+    if (step) *step = m->m->step;
+  });
+}
+
+int aur_model_state_load(aur_model* m, const void* src, uint64_t step) {
+  if (!m || !src) return AUR_EINVAL;
+  return guard(m->m->ctx(), [&] {
+    m->m->copy_state_from(src);
+    m->m->step = step;
   });
 }
 
@@ -971,7 +1072,7 @@ int aur_model_eval_step_batch(aur_model* m, const uint32_t* tokens, const uint32
 int aur_model_clip_grads(aur_model* m, float max_norm, float* norm) {
   if (!m) return AUR_EINVAL;
   return guard(m->m->ctx(), [&] {
-    float n = m->m->clip_grads(max_norm);
+    float n = m->m->clip_grads(max_norm, norm != nullptr);
     if (norm) *norm = n;
   });
 }
@@ -985,7 +1086,8 @@ int aur_model_clip_step_adamw(aur_model* m, float max_norm, float lr, float beta
                               float weight_decay, float* norm) {
   if (!m) return AUR_EINVAL;
   return guard(m->m->ctx(), [&] {
-    float n = m->m->clip_and_step_adamw(max_norm, aurora::AdamWConfig{lr, beta1, beta2, eps, weight_decay});
+    float n = m->m->clip_and_step_adamw(max_norm, aurora::AdamWConfig{lr, beta1, beta2, eps, weight_decay},
+                                        norm != nullptr);
     if (norm) *norm = n;
   });
 }
@@ -993,12 +1095,12 @@ int aur_model_clip_step_adamw(aur_model* m, float max_norm, float lr, float beta
 int aur_kv_cache_create(aur_model* m, uint32_t batch, uint32_t max_len, aur_kv_cache** out) {
   if (!m || !out) return AUR_EINVAL;
   *out = nullptr;
-  return guard(m->m->ctx(), [&] { *out = new aur_kv_cache{new KvCacheGpu(*m->m, batch, max_len), m}; });
+  return guard(m->m->ctx(), [&] { *out = new aur_kv_cache{new KvCacheGpu(*m->m, batch, max_len), m->m->ctx()}; });
 }
 
 int aur_kv_cache_reset(aur_kv_cache* c) {
   if (!c) return AUR_EINVAL;
-  return guard(c->owner->m->ctx(), [&] { c->c->reset(); });
+  return guard(c->ctx, [&] { c->c->reset(); });
 }
 
 int aur_kv_cache_destroy(aur_kv_cache* c) {

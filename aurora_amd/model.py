@@ -95,9 +95,9 @@ class DecoderTransformerGpu:
         self._call("aur_model_step_muon_hybrid", muon_lr, momentum, 1 if nesterov else 0, muon_wd,
                    ns_steps, lr, beta1, beta2, eps, weight_decay)
 
-    def clip_grads_adamw_subset(self, max_norm: float) -> float:
-        n = C.c_float()
-        self._call("aur_model_clip_grads_adamw_subset", max_norm, C.byref(n))
+    def clip_grads_adamw_subset(self, max_norm: float, want_norm: bool = True) -> float:
+        n = C.c_float(float("nan"))
+        self._call("aur_model_clip_grads_adamw_subset", max_norm, C.byref(n) if want_norm else None)
         return n.value
 
     # ---- AURORA07 checkpoints (src/checkpoint.rs) ----
@@ -121,12 +121,48 @@ class DecoderTransformerGpu:
         m.load_checkpoint(path)
         return m
 
-    def train_step_batch(self, tokens, targets) -> float:
+    def train_step_batch(self, tokens, targets, reduction: str = "mean") -> float:
+        """Forward + CE + backward of b sequences; grads accumulate, combined
+        over the batch as their mean ("mean", the CPU trainer) or their sum
+        ("sum", src/gpu/transformer.rs:1555-1559).  Returns Σ_b mean_t NLL."""
+        red = {"mean": 0, "sum": 1}[reduction]
         tok, tgt = _u32(tokens), _u32(targets)
         b, t = tok.shape
         loss = C.c_float()
-        self._call("aur_model_train_step_batch", tok.ctypes.data, tgt.ctypes.data, b, t, C.byref(loss))
+        self._call("aur_model_train_step_batch_ex", tok.ctypes.data, tgt.ctypes.data, b, t, red,
+                   C.byref(loss))
         return loss.value
+
+    def train_step(self, tokens, targets) -> float:
+        """Single sequence (src/gpu/transformer.rs:1535): mean-over-t loss."""
+        return self.train_step_batch(np.asarray(tokens)[None, :], np.asarray(targets)[None, :], "sum")
+
+    def grad_norm(self) -> float:
+        n = C.c_float()
+        self._call("aur_model_grad_norm", C.byref(n))
+        return n.value
+
+    # ---- state snapshot (src/gpu/transformer.rs:1152-1240) ----
+    def state_bytes(self) -> int:
+        n = C.c_size_t()
+        self._call("aur_model_state_bytes", C.byref(n))
+        return n.value
+
+    def snapshot_state(self):
+        """A device buffer holding the parameters and optimizer state (its .step
+        attribute the optimizer step), copied on the device."""
+        from .gpu import GpuBuffer
+        buf = GpuBuffer.empty(self.ctx, self.state_bytes() // 4)
+        self.refresh_state(buf)
+        return buf
+
+    def refresh_state(self, buf) -> None:
+        st = C.c_uint64()
+        self._call("aur_model_state_save", buf.ptr, C.byref(st))
+        buf.step = st.value
+
+    def restore_state(self, buf) -> None:
+        self._call("aur_model_state_load", buf.ptr, buf.step)
 
     def forward(self, tokens, want_logits: bool = True):
         tok = _u32(tokens)
@@ -164,9 +200,9 @@ class DecoderTransformerGpu:
             s = np.float32(s + x)
         return float(s)
 
-    def clip_grads(self, max_norm: float) -> float:
-        n = C.c_float()
-        self._call("aur_model_clip_grads", max_norm, C.byref(n))
+    def clip_grads(self, max_norm: float, want_norm: bool = True) -> float:
+        n = C.c_float(float("nan"))
+        self._call("aur_model_clip_grads", max_norm, C.byref(n) if want_norm else None)
         return n.value
 
     def step_adamw(self, lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1) -> None:

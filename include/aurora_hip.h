@@ -220,8 +220,20 @@ int aur_model_load_checkpoint(aur_model* m, const char* path, uint32_t* epoch, u
 int aur_model_save_checkpoint(aur_model* m, const char* path, uint32_t epoch, uint64_t step);
 /* train_step_batch (transformer.rs:1571): forward + softmax-CE + backward for
  * b host sequences of length t (tokens/targets [b*t]); gradients accumulate
- * as the batch MEAN of per-sequence mean-over-t losses (the CPU trainer's
- * convention, examples/aurora_train.rs:840-846).  *loss_sum = Σ_b mean_t NLL. */
+ * (+=, zero_grad first).  Each sequence's loss is its mean-over-t NLL
+ * (model.rs:820-858); `reduction` says how the b gradients combine:
+ *   AUR_BATCH_SUM  — summed, the reference GPU model's convention
+ *                    (transformer.rs:1555-1559; its trainer then clips at
+ *                    B × the threshold, examples/aurora_train.rs:1046-1051);
+ *   AUR_BATCH_MEAN — averaged, the CPU trainer's grads.scale(1/B)
+ *                    (examples/aurora_train.rs:840-846).
+ * train_step (transformer.rs:1535) is the b = 1 case of either.
+ * *loss_sum = Σ_b mean_t NLL_b (the reference's return value). */
+#define AUR_BATCH_MEAN 0u
+#define AUR_BATCH_SUM 1u
+int aur_model_train_step_batch_ex(aur_model* m, const uint32_t* tokens, const uint32_t* targets,
+                                  uint32_t b, uint32_t t, uint32_t reduction, float* loss_sum);
+/* The AUR_BATCH_MEAN form of aur_model_train_step_batch_ex. */
 int aur_model_train_step_batch(aur_model* m, const uint32_t* tokens, const uint32_t* targets,
                                uint32_t b, uint32_t t, float* loss_sum);
 /* Forward only (encode_forward, transformer.rs:1347); logits [b*t, vocab]
@@ -234,8 +246,13 @@ int aur_model_forward(aur_model* m, const uint32_t* tokens, uint32_t b, uint32_t
  * gradients and optimizer state are left untouched. */
 int aur_model_eval_step_batch(aur_model* m, const uint32_t* tokens, const uint32_t* targets,
                               uint32_t b, uint32_t t, float* nll);
+/* grad_norm (transformer.rs:1263): global L2 norm over all gradients. */
+int aur_model_grad_norm(aur_model* m, float* norm);
 /* clip_grads (model.rs:1011-1017): global L2 over all gradients, scaled in
- * place when above max_norm; *norm = the pre-clip norm. */
+ * place when above max_norm; *norm = the pre-clip norm.  With norm == NULL
+ * the norm is not read back (no host synchronisation), like the reference's
+ * want_norm = false (transformer.rs:2294); the same holds for the other
+ * clipping entry points below. */
 int aur_model_clip_grads(aur_model* m, float max_norm, float* norm);
 /* step_adamw (model.rs:926-1009, transformer.rs:2008). */
 int aur_model_step_adamw(aur_model* m, float lr, float beta1, float beta2, float eps,
@@ -257,9 +274,21 @@ int aur_model_clip_grads_adamw_subset(aur_model* m, float max_norm, float* norm)
 /* clip_grads + step_adamw fused (the clip factor is applied inside AdamW). */
 int aur_model_clip_step_adamw(aur_model* m, float max_norm, float lr, float beta1, float beta2,
                               float eps, float weight_decay, float* norm);
+/* snapshot_state / refresh_state / restore_state (transformer.rs:1152-1240):
+ * the persistent state — parameters, both AdamW moments and, once allocated,
+ * the Muon momentum — copied device-to-device into / out of a caller-owned
+ * DEVICE buffer of aur_model_state_bytes bytes (enqueued, no host sync);
+ * the optimizer step counter is returned / set alongside. */
+int aur_model_state_bytes(aur_model* m, size_t* bytes);
+int aur_model_state_save(aur_model* m, void* dst, uint64_t* step);
+int aur_model_state_load(aur_model* m, const void* src, uint64_t step);
 
 /* KvCacheGpu::new (kv_cache.rs:42) for `batch` sequences decoded together,
- * max_len <= seq_len_max; reset zeroes it (kv_cache.rs:76). */
+ * max_len <= seq_len_max; reset zeroes it (kv_cache.rs:76).  A cache serves
+ * only the model it was created from (prefill / generate_step with another
+ * model return AUR_EINVAL).  Destroying the model detaches its caches: they
+ * then accept only aur_kv_cache_destroy (and reset / len / history), and
+ * decoding with them returns AUR_EINVAL. */
 int aur_kv_cache_create(aur_model* m, uint32_t batch, uint32_t max_len, aur_kv_cache** out);
 int aur_kv_cache_reset(aur_kv_cache* c);
 int aur_kv_cache_destroy(aur_kv_cache* c);

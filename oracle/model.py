@@ -166,20 +166,46 @@ def backward(P: dict, cfg: Config, cache: dict, logits, targets, G: dict) -> flo
     return total / t
 
 
-def batch_grads(P: dict, cfg: Config, tokens, targets):
+def sequence_grads(P: dict, cfg: Config, tokens, targets):
+    """Forward + backward of one sequence into fresh grads → (mean NLL, g)."""
+    g = zeros_like(P)
+    logits, cache = forward(P, cfg, tokens)
+    loss = backward(P, cfg, cache, logits, targets, g)
+    return loss, g
+
+
+def batch_grads(P: dict, cfg: Config, tokens, targets, threads: int = 1, reduction: str = "mean"):
     """aurora_train.rs:812-846 without the optimizer: per-sequence grads summed
-    in sequence order then scaled by 1/B.  Returns (Σ_b loss_b, G)."""
+    in sequence order, then scaled by 1/B ("mean", the CPU trainer) or left
+    summed ("sum", the GPU model's train_step_batch, gpu/transformer.rs:
+    1555-1559).  Returns (Σ_b loss_b, G).
+
+    threads > 1 computes the sequences concurrently, as the reference's rayon
+    par_iter does (aurora_train.rs:828-838); each sequence's arithmetic and
+    the in-order sum are unchanged, so the result is bit-identical."""
     tokens = np.asarray(tokens, np.uint32)
     targets = np.asarray(targets, np.uint32)
     B = tokens.shape[0]
     G = zeros_like(P)
     loss = 0.0
-    for b in range(B):
-        g = zeros_like(P)
-        logits, cache = forward(P, cfg, tokens[b])
-        loss += backward(P, cfg, cache, logits, targets[b], g)
-        _add_assign(G, g)
-    scale_grads(G, 1.0 / B)
+    if threads <= 1 or B == 1:
+        results = (sequence_grads(P, cfg, tokens[b], targets[b]) for b in range(B))
+        for lb, g in results:
+            loss += lb
+            _add_assign(G, g)
+    else:
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(max_workers=min(threads, B)) as ex:
+            futs = [ex.submit(sequence_grads, P, cfg, tokens[b], targets[b]) for b in range(B)]
+            for f in futs:  # summed in sequence order
+                lb, g = f.result()
+                loss += lb
+                _add_assign(G, g)
+                del g
+    if reduction == "mean":
+        scale_grads(G, 1.0 / B)
+    elif reduction != "sum":
+        raise ValueError(reduction)
     return loss, G
 
 

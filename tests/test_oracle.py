@@ -268,3 +268,21 @@ def test_batch_grads_are_mean_of_sequences():
     for (_, _, gb), (_, _, g0), (_, _, g1) in zip(OM.tensors(G), OM.tensors(singles[0]),
                                                  OM.tensors(singles[1])):
         np.testing.assert_allclose(gb, (g0 + g1) / 2, rtol=0, atol=1e-6)
+
+
+def test_batch_grads_threads_and_sum_mode():
+    """The threaded oracle (sequences concurrently, summed in sequence order)
+    is bit-identical to the serial one; the sum mode is the mean mode times B
+    (the GPU model's convention, gpu/transformer.rs:1555-1559)."""
+    cfg = TINY
+    P = OM.init_params(cfg, 12)
+    rng = np.random.default_rng(12)
+    tok = rng.integers(0, cfg.vocab, (4, 9)).astype(np.uint32)
+    tgt = rng.integers(0, cfg.vocab, (4, 9)).astype(np.uint32)
+    l1, G1 = OM.batch_grads(P, cfg, tok, tgt)
+    l4, G4 = OM.batch_grads(P, cfg, tok, tgt, threads=4)
+    ls, Gs = OM.batch_grads(P, cfg, tok, tgt, threads=3, reduction="sum")
+    assert l1 == l4 == ls
+    for (_, _, a), (_, _, b), (_, _, s) in zip(OM.tensors(G1), OM.tensors(G4), OM.tensors(Gs)):
+        assert np.array_equal(a, b)
+        np.testing.assert_allclose(s, 4 * a.astype(np.float64), rtol=1e-6, atol=1e-9)
