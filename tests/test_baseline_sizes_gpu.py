@@ -84,7 +84,8 @@ def test_config3_full_model_directional_derivatives(ctx):
     del P
     m.zero_grad()
     loss = m.train_step_batch(tok, tgt) / 16  # mean-mode grads: ∇ of this mean loss
-    assert abs(loss - np.log(C3.vocab)) < 0.1, loss
+    # logits at init have std ≈ 0.64, so E[NLL] ≈ ln V + σ²/2 ≈ 9.2
+    assert abs(loss - np.log(C3.vocab)) < 0.5, loss
     g_all = m.get("grads")
     assert np.all(np.isfinite(g_all))
     # bitwise repeatable
