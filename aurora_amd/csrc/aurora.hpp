@@ -343,6 +343,7 @@ class KvCacheGpu {
   float* part_ = nullptr;  // K-range partial products of the W_o / W_proj decode GEMMs
   size_t part_floats_ = 0;
   int qkv_parts = 1;  // K ranges of the decode QKV projection held in qkv_
+  int o_parts = 1, p_parts = 1;  // K ranges of the W_o / W_proj products in part_
   size_t bytes_ = 0;
   void* graph_ = nullptr;       // hipGraphExec_t of one decode step, built on first use
 };

@@ -730,7 +730,7 @@ __global__ void __launch_bounds__(256) wide_partials_kernel(GemmArgs g) {
 }
 
 // ------------------------------------ decode K-range partials, short ranges
-// P[z][M ≤ 16·MT][N] for K range z of KR (64 or 128) and N % 64 == 0.  A
+// P[z][M ≤ 16·MT][N] for K range z of KR (64, 128 or 256) and N % 64 == 0.  A
 // 256-thread block owns 64 columns (16 per wave) and one range.  Each wave
 // issues every W load of its 16 rows × KR first (coalesced: lanes 4r..4r+3
 // read row r's 64 contiguous bytes per 16-k chunk, moved into the MFMA
@@ -1142,13 +1142,16 @@ int gemm_nt_partials(aur_ctx* ctx, const float* A, int lda, const float* B, int 
   a.A = A; a.B = B; a.P = P; a.M = M; a.N = N; a.K = K;
   a.lda = lda; a.ldb = ldb; a.k_chunk = chunk;
   dim3 grid((N + 63) / 64, splits);
-  if ((chunk == 64 || chunk == 128) && N % 64 == 0 && K % chunk == 0) {
+  const bool stream = (chunk == 64 || chunk == 128 || chunk == 256) && N % 64 == 0 && K % chunk == 0;
+  if (stream) {
 #define AUR_STREAM_PARTIALS(MT)                                                                  \
   do {                                                                                            \
     if (chunk == 64)                                                                              \
       hipLaunchKernelGGL((stream_partials_kernel<MT, 64>), grid, dim3(256), 0, ctx->stream, a);  \
-    else                                                                                          \
+    else if (chunk == 128)                                                                        \
       hipLaunchKernelGGL((stream_partials_kernel<MT, 128>), grid, dim3(256), 0, ctx->stream, a); \
+    else                                                                                          \
+      hipLaunchKernelGGL((stream_partials_kernel<MT, 256>), grid, dim3(256), 0, ctx->stream, a); \
   } while (0)
     if (M <= 16)
       AUR_STREAM_PARTIALS(1);

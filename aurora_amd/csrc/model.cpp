@@ -14,6 +14,8 @@
 // device; the host reads back only the per-row NLL (one small copy per step).
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <numeric>
 #include <vector>
@@ -46,15 +48,29 @@ inline void hip_ck(aur_ctx* ctx, hipError_t e, const char* what) {
   if (e != hipSuccess) check(ctx, aur::set_error(ctx, (int)e, "%s: %s", what, hipGetErrorString(e)), what);
 }
 
-// K ranges of the decode QKV projection (K = d_model): ranges of 128, at most
-// 8, tiling K the way gemm_nt_partials does (multiples of 64).
-int qkv_splits(size_t d) {
-  int s = (int)std::max<size_t>(1, std::min<size_t>(8, d / 128));
-  for (; s > 1; --s) {
-    const size_t chunk = ((d + s - 1) / s + 63) / 64 * 64;
-    if ((d + chunk - 1) / chunk == (size_t)s) break;
+// The largest split count <= s whose K ranges (multiples of 64, as
+// gemm_nt_partials cuts them) are all non-empty.
+int fit_splits(size_t K, int s) {
+  for (s = std::max(s, 1); s > 1; --s) {
+    const size_t chunk = ((K + s - 1) / s + 63) / 64 * 64;
+    if ((K + chunk - 1) / chunk == (size_t)s) break;
   }
   return s;
+}
+
+// K ranges of the decode QKV projection (K = d_model): ranges of 128, at most
+// 8 (the attention kernel sums at most 8).
+int qkv_splits(size_t d) { return fit_splits(d, (int)std::max<size_t>(1, std::min<size_t>(8, d / 128))); }
+
+// AUR_DEC_SPLITS = "q:o:p" overrides the decode step's split counts (QKV,
+// W_o, W_proj; 0 keeps the default) for tuning; read when a cache is
+// created.
+int split_override(int which, int dflt, size_t K, int cap) {
+  const char* env = std::getenv("AUR_DEC_SPLITS");
+  if (!env) return dflt;
+  int v[3] = {0, 0, 0};
+  if (std::sscanf(env, "%d:%d:%d", &v[0], &v[1], &v[2]) < 1 || v[which] <= 0) return dflt;
+  return fit_splits(K, std::min(v[which], cap));
 }
 
 }  // namespace
@@ -678,17 +694,19 @@ KvCacheGpu::KvCacheGpu(DecoderTransformerGpu& model, uint32_t batch_, uint32_t m
   const size_t B = batch, d = d_model, F = c.d_ff, V = c.vocab;
   const size_t hist = (size_t)n_layer * B * max_len * d;
   const size_t scratch = (aur_mha_kv_ws_bytes(batch, c.n_head, max_len) + 3) / 4;
-  // K-range partial products of the W_o / W_proj decode GEMMs: [splits][B][d].
-  part_floats_ = (size_t)std::max(aur::gemm_nt_partials_splits((int)B, (int)d, (int)d),
-                                  aur::gemm_nt_partials_splits((int)B, (int)d, (int)F)) *
-                 B * d;
-  // The decode QKV projection as qkv_parts K-range partials [parts][B][3d]
-  // that the attention kernel sums (B ≤ 64), else one product.
-  qkv_parts = batch <= 64 ? qkv_splits(d) : 1;
+  if (batch <= 64) {
+    // The decode QKV projection as qkv_parts K-range partials [parts][B][3d]
+    // that the attention kernel sums; W_o / W_proj as K-range partials
+    // [splits][B][d] that the following LayerNorm sums.
+    qkv_parts = split_override(0, qkv_splits(d), d, 8);
+    o_parts = split_override(1, aur::gemm_nt_partials_splits((int)B, (int)d, (int)d), d, 64);
+    p_parts = split_override(2, aur::gemm_nt_partials_splits((int)B, (int)d, (int)F), F, 64);
+  }
+  part_floats_ = (size_t)std::max(o_parts, p_parts) * B * d;
   // x, ln, qkv (3 per part), attn, xmid rows of d per sequence
   const size_t floats =
       2 * hist + B * (d * (4 + 3 * (size_t)qkv_parts) + 2 * F + V) + scratch + part_floats_;
-  bytes_ = floats * 4 + 3 * B * 4 + 32 * 256;
+  bytes_ = floats * 4 + 3 * B * 4 + 40 * 256;
   ck(ctx_, aur_malloc(ctx_, bytes_, &mem_), "KvCacheGpu alloc");
   Carver cv{static_cast<char*>(mem_)};
   k_ = cv.take<float>(hist);
@@ -826,11 +844,12 @@ void DecoderTransformerGpu::encode_decode_step(KvCacheGpu& cache) {
   // following LayerNorm sums (with the residual add) — more blocks in flight
   // and no separate reduction launch.
   const bool split = cache.batch <= 64;
-  const int s_o = aur::gemm_nt_partials_splits(B, d, d), s_p = aur::gemm_nt_partials_splits(B, d, F);
-  // h = w_tok[tok] + w_pos[pos]  (kv_cache.rs:103-115)
-  // (and lens = pos + 1 for the attention below)
-  ck(ctx_, aur::embed_forward(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, 0, cache.x_, B, d, cache.lens_),
-     "embed");
+  const int s_o = cache.o_parts, s_p = cache.p_parts;
+  // h = w_tok[tok] + w_pos[pos]  (kv_cache.rs:103-115), lens = pos + 1 for
+  // the attention below, and the first block's LayerNorm of h
+  ck(ctx_, aur::embed_layer_norm(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, cache.x_, (*layers_)[0].ln1_g,
+                                 (*layers_)[0].ln1_b, cache.ln_, cache.lens_, B, d, kLnEps),
+     "embed + ln1");
   // Attention is launched for lengths up to max_len (keys past a sequence's
   // length are skipped on the device), so the launch shape is the same for
   // every step.
@@ -842,7 +861,7 @@ void DecoderTransformerGpu::encode_decode_step(KvCacheGpu& cache) {
       ck(ctx_, aur::layer_norm_forward_sum(ctx_, cache.xmid_, cache.part_, s_p, cache.x_, Y.ln1_g, Y.ln1_b,
                                            cache.ln_, B, d, kLnEps),
          "ln1");
-    else
+    else if (l > 0)
       ck(ctx_, aur::layer_norm_forward(ctx_, cache.x_, Y.ln1_g, Y.ln1_b, cache.ln_, nullptr, nullptr, B, d,
                                        kLnEps),
          "ln1");

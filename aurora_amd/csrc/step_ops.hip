@@ -798,6 +798,124 @@ __global__ void __launch_bounds__(256) argmax_kernel(const float* __restrict__ l
   }
 }
 
+// The same for V % 4 == 0 with 16-byte aligned rows; the kernel can also
+// complete a split-K product first: logits = P[0] + … + P[np−1] (summed in
+// range order, written to `logits` when P is not that buffer).  Each thread
+// holds 8 float4 columns per pass, all loads of a pass issued together; the
+// (value, index) pairs reduce across the block, ties to the lower index.
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+__global__ void __launch_bounds__(256) argmax_sum_kernel(const float* __restrict__ P, int np, size_t pstride,
+                                                         float* __restrict__ logits, int V,
+                                                         uint32_t* __restrict__ out, int32_t* __restrict__ pos) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const float* pr = P + (size_t)r * V;
+  float* lr = logits + (size_t)r * V;
+  const bool store = P != logits;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int c0 = 0; c0 < V; c0 += 8 * 1024) {
+    floatx4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = c0 + 1024 * j + 4 * tid;
+      floatx4 a = {0.f, 0.f, 0.f, 0.f};
+      if (c < V) {
+        a = *reinterpret_cast<const floatx4*>(pr + c);
+        for (int z = 1; z < np; ++z) a += *reinterpret_cast<const floatx4*>(pr + z * pstride + c);
+        if (store) *reinterpret_cast<floatx4*>(lr + c) = a;
+      }
+      v[j] = a;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = c0 + 1024 * j + 4 * tid;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c + e < V && v[j][e] > best) {  // ascending columns: strict > keeps the first
+          best = v[j][e];
+          bi = c + e;
+        }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    argmax_merge(best, bi, ov, oi);
+  }
+  if ((tid & 63) == 0) {
+    sv[tid >> 6] = best;
+    si[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w) argmax_merge(best, bi, sv[w], si[w]);
+    out[r] = (uint32_t)(bi == 0x7fffffff ? 0 : bi);
+    if (pos) pos[r] += 1;
+  }
+}
+
+// Decode step input: x = w_tok[tok] + w_pos[pos] (kv_cache.rs:103-115), lens =
+// pos + 1, and y = LN(x) with the first block's γ/β — the embedding and the
+// first LayerNorm in one launch.  One block per row, d % 4 == 0, d <= 4096.
+__global__ void __launch_bounds__(256) embed_ln_kernel(const float* __restrict__ w_tok,
+                                                       const float* __restrict__ w_pos,
+                                                       const uint32_t* __restrict__ tok,
+                                                       const int32_t* __restrict__ pos_dev,
+                                                       float* __restrict__ xo, const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta, float* __restrict__ y,
+                                                       int32_t* __restrict__ lens, int d, float eps) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const int p = pos_dev[r];
+  if (lens && threadIdx.x == 0) lens[r] = p + 1;
+  const float* a = w_tok + (size_t)tok[r] * d;
+  const float* b = w_pos + (size_t)p * d;
+  floatx4 xv[4];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (threadIdx.x + 256 * i) * 4;
+    floatx4 v = {0.f, 0.f, 0.f, 0.f};
+    if (c < d) {
+      v = *reinterpret_cast<const floatx4*>(a + c) + *reinterpret_cast<const floatx4*>(b + c);
+      *reinterpret_cast<floatx4*>(xo + (size_t)r * d + c) = v;
+      s += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+    xv[i] = v;
+  }
+  const float mu = block_sum(s, red) / (float)d;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (threadIdx.x + 256 * i) * 4;
+    if (c < d)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q += (xv[i][e] - mu) * (xv[i][e] - mu);
+  }
+  const float is = 1.0f / sqrtf(block_sum(q, red) / (float)d + eps);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (threadIdx.x + 256 * i) * 4;
+    if (c < d) {
+      const floatx4 gg = *reinterpret_cast<const floatx4*>(gamma + c);
+      const floatx4 bb = *reinterpret_cast<const floatx4*>(beta + c);
+      floatx4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (xv[i][e] - mu) * is * gg[e] + bb[e];
+      *reinterpret_cast<floatx4*>(y + (size_t)r * d + c) = o;
+    }
+  }
+}
+
 __global__ void gather_rows_kernel(const float* __restrict__ src, int ld_src, int row_step,
                                    int row_off, float* __restrict__ dst, int rows, int d) {
   const int r = blockIdx.x;
@@ -1004,8 +1122,23 @@ int kv_store(aur_ctx* ctx, const float* qkv, int d, float* kh, float* vh, int ma
 }
 
 int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out, int32_t* pos) {
+  if (V % 4 == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0) {
+    hipLaunchKernelGGL(argmax_sum_kernel, dim3(rows), dim3(256), 0, ctx->stream, logits, 1, (size_t)0,
+                       const_cast<float*>(logits), V, out, pos);
+    LAUNCH_OK(ctx, "argmax_sum_kernel");
+  }
   hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, ctx->stream, logits, V, out, pos);
   LAUNCH_OK(ctx, "argmax_kernel");
+}
+
+int embed_layer_norm(aur_ctx* ctx, const float* w_tok, const float* w_pos, const uint32_t* tok,
+                     const int32_t* pos_dev, float* x_out, const float* gamma, const float* beta, float* y,
+                     int32_t* lens, int rows, int d, float eps) {
+  if (d % 4 != 0 || d > 4096 || !pos_dev)
+    return set_error(ctx, AUR_EINVAL, "embed_layer_norm: d=%d unsupported", d);
+  hipLaunchKernelGGL(embed_ln_kernel, dim3(rows), dim3(256), 0, ctx->stream, w_tok, w_pos, tok, pos_dev, x_out,
+                     gamma, beta, y, lens, d, eps);
+  LAUNCH_OK(ctx, "embed_ln_kernel");
 }
 
 int gather_rows(aur_ctx* ctx, const float* src, int ld_src, int row_step, int row_off, float* dst,

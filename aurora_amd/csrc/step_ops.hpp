@@ -56,6 +56,10 @@ int kv_store(aur_ctx* ctx, const float* qkv, int d, float* kh, float* vh, int ma
              const int32_t* pos_dev, int rows, int T);
 // out[r] = first argmax of logits row r; pos[r] += 1 when pos is non-null.
 int argmax_rows(aur_ctx* ctx, const float* logits, int rows, int V, uint32_t* out, int32_t* pos = nullptr);
+// Decode input row: x = w_tok[tok] + w_pos[pos], lens = pos + 1, y = LN(x).
+int embed_layer_norm(aur_ctx* ctx, const float* w_tok, const float* w_pos, const uint32_t* tok,
+                     const int32_t* pos_dev, float* x_out, const float* gamma, const float* beta, float* y,
+                     int32_t* lens, int rows, int d, float eps);
 // dst[r] = src[(r*row_step + row_off) * ld_src .. + d]
 int gather_rows(aur_ctx* ctx, const float* src, int ld_src, int row_step, int row_off, float* dst,
                 int rows, int d);
