@@ -36,6 +36,7 @@ SIGNATURES: dict[str, tuple] = {
     "aur_gemm_nn": (_i32, [_c_ctx, _f, _f, _f, _u32, _u32, _u32]),
     "aur_gemm_nt": (_i32, [_c_ctx, _f, _f, _f, _u32, _u32, _u32]),
     "aur_outer_accum": (_i32, [_c_ctx, _f, _f, _f, _u32, _u32, _u32]),
+    "aur_outer_accum_noalloc": (_i32, [_c_ctx, _f, _f, _f, _u32, _u32, _u32]),
     "aur_gemm_ex": (_i32, [_c_ctx, _i32, _i32, _f, _u32, _f, _u32, _f, _u32,
                            _u32, _u32, _u32, _i32]),
     "aur_mha_fwd": (_i32, [_c_ctx, _f, _f, _f, _f, _f, _u32, _u32, _u32, _u32]),

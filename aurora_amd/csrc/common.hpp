@@ -20,6 +20,11 @@ struct aur_ctx {
   std::string last_error;
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // This device's copy of the allocation-free entry point's scratch array
+  // (its device address, from hipGetSymbolAddress at aur_init), or null with
+  // the failing call's code in noalloc_err.
+  float* noalloc_scratch = nullptr;
+  int noalloc_err = 0;
 };
 
 namespace aur {
@@ -28,6 +33,10 @@ int set_error(aur_ctx* ctx, int code, const char* fmt, ...);
 
 // Makes `ctx` own at least `bytes` of workspace; returns 0 or an error code.
 int ensure_workspace(aur_ctx* ctx, size_t bytes);
+
+// Looks up (once per device, with that device current) the device address of
+// the allocation-free entry point's scratch array and stores it in ctx.
+void noalloc_scratch_init(aur_ctx* ctx);
 
 // Output forms fused into the GEMM store; v = (A·B)(row, col), and R, X, C2
 // are addressed with C's leading dimension.

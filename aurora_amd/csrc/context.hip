@@ -89,6 +89,7 @@ int aur_init(int device, aur_ctx** out) {
   aur_ctx* ctx = new aur_ctx();
   ctx->device = device;
   ctx->cu_count = prop.multiProcessorCount;
+  aur::noalloc_scratch_init(ctx);
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;

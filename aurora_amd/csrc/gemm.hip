@@ -22,6 +22,9 @@
 // no atomics — and adds into the destination.
 #include "common.hpp"
 
+#include <map>
+#include <mutex>
+
 #include <algorithm>
 #include <cstdlib>
 
@@ -918,7 +921,34 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
+// Scratch of aur_outer_accum_noalloc: the split-K partial tiles of one call,
+// 2^24 floats (64 MiB) on every device the library runs on, held until the
+// process ends.  Host code never uses this name as an address (on the host it
+// is only a stand-in for the symbol): it takes each device's address from
+// hipGetSymbolAddress once, at aur_init, and passes that to the kernels.
+constexpr size_t kNoAllocScratchFloats = size_t(1) << 24;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
 namespace aur {
+
+void noalloc_scratch_init(aur_ctx* ctx) {
+  static std::mutex mu;
+  static std::map<int, float*> per_device;  // device → address of its copy of `scratch`
+  std::lock_guard<std::mutex> g(mu);
+  auto it = per_device.find(ctx->device);
+  if (it != per_device.end()) {
+    ctx->noalloc_scratch = it->second;
+    return;
+  }
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr) {
+    ctx->noalloc_err = e != hipSuccess ? (int)e : AUR_ENOMEM;
+    return;
+  }
+  per_device[ctx->device] = static_cast<float*>(ptr);
+  ctx->noalloc_scratch = static_cast<float*>(ptr);
+}
 
 // Split-K partial tiles: the caller's workspace (ws) or the context's
 // grow-only one.
@@ -1198,6 +1228,28 @@ int aur_outer_accum(aur_ctx* ctx, const float* x, const float* d_y, float* dest,
   // and B(t,i) = x[t*d_in + i] (k-strided).
   return aur::gemm(ctx, false, false, d_y, (int)d_out, x, (int)d_in, dest, (int)d_in, (int)d_out,
                    (int)d_in, (int)t, true);
+}
+
+int aur_outer_accum_noalloc(aur_ctx* ctx, const float* x, const float* d_y, float* dest, uint32_t d_out,
+                            uint32_t d_in, uint32_t t) {
+  AUR_CHECK_CTX(ctx);
+  if (!ctx->noalloc_scratch)
+    return aur::set_error(ctx, ctx->noalloc_err ? ctx->noalloc_err : AUR_ENOMEM,
+                          "aur_outer_accum_noalloc: no scratch on device %d (hipGetSymbolAddress: %s)", ctx->device,
+                          hipGetErrorString((hipError_t)ctx->noalloc_err));
+  // The same launch plan and kernels as aur_outer_accum, with the split-K
+  // partials in the device's scratch array instead of the context workspace.
+  const aur::Workspace ws{ctx->noalloc_scratch, kNoAllocScratchFloats};
+  aur::Epilogue e;
+  e.mode = aur::EPI_ACCUM;
+  const int rc = aur::gemm(ctx, false, false, d_y, (int)d_out, x, (int)d_in, dest, (int)d_in, (int)d_out, (int)d_in,
+                           (int)t, e, &ws);
+  if (rc == AUR_ENOMEM)  // the plan's partial tiles exceed the scratch: nothing was launched
+    return aur::set_error(ctx, AUR_ELIMIT,
+                          "aur_outer_accum_noalloc: d_out=%u d_in=%u t=%u needs more than the %zu floats of "
+                          "scratch (%s)",
+                          d_out, d_in, t, kNoAllocScratchFloats, ctx->last_error.c_str());
+  return rc;
 }
 
 int aur_gemm_ex(aur_ctx* ctx, int a_kcontig, int b_kcontig, const float* a, uint32_t lda,

@@ -95,6 +95,22 @@ int aur_gemm_nt(aur_ctx* ctx, const float* a, const float* b, float* c,
 int aur_outer_accum(aur_ctx* ctx, const float* x, const float* d_y, float* dest,
                     uint32_t d_out, uint32_t d_in, uint32_t t);
 
+/* aur_outer_accum without any allocation: the same arithmetic (same launch
+ * plan and kernels, so the same result bit for bit), with the split-K
+ * partial tiles in a fixed scratch array the library holds on each device
+ * (2^24 floats = 64 MiB, a file-scope __device__ array, present from library
+ * load until the process ends) instead of the context's grow-on-demand
+ * workspace.  It calls no hipMalloc / hipFree and never synchronises.
+ * No counterpart in the reference: it is for callers that cannot allocate —
+ * work captured into a HIP graph, tight serving loops, harnesses that
+ * forbid allocation.  Shapes whose partial tiles need more than the scratch
+ * return AUR_ELIMIT before anything is launched.  Every call on one device
+ * shares that device's array; nothing in it needs clearing (each call writes
+ * the partial tiles it reads back), but calls that overlap on one device —
+ * from two contexts' streams, say — race on it. */
+int aur_outer_accum_noalloc(aur_ctx* ctx, const float* x, const float* d_y, float* dest,
+                            uint32_t d_out, uint32_t d_in, uint32_t t);
+
 /* General strided form used by the model orchestrator (no reference
  * counterpart as one call: it is the union of the three kernels above with
  * explicit leading dimensions).
