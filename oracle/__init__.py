@@ -287,6 +287,8 @@ def token_nll(logits, targets, v) -> np.ndarray:
 
 def embed_forward(w_tok, w_pos, tokens, d) -> np.ndarray:
     w_tok, w_pos, tokens = f32(w_tok), f32(w_pos), u32(tokens)
+    if tokens.size * d > w_pos.size or (tokens.size and int(tokens.max()) * d >= w_tok.size):
+        raise ValueError(f"embed_forward: {tokens.size} positions / token ids past the tables")
     out = np.empty(tokens.size * d, np.float32)
     lib().ora_embed_forward(_p(w_tok), _p(w_pos), _p(tokens), _p(out), tokens.size, d)
     return out
@@ -294,6 +296,8 @@ def embed_forward(w_tok, w_pos, tokens, d) -> np.ndarray:
 
 def embed_backward(tokens, dy, d_w_tok, d_w_pos, d) -> None:
     tokens, dy = u32(tokens), f32(dy)
+    if tokens.size * d > d_w_pos.size or (tokens.size and int(tokens.max()) * d >= d_w_tok.size):
+        raise ValueError(f"embed_backward: {tokens.size} positions / token ids past the tables")
     lib().ora_embed_backward(_p(tokens), _p(dy), _p(d_w_tok), _p(d_w_pos), tokens.size, d)
 
 

@@ -59,3 +59,10 @@ def test_workspace_size_helpers():
     assert lib.aur_mha_bwd_ws_bytes(16, 1024, 8) == (16 * 1024 * 8 + 16 * 8 * 136 * 4096) * 4
     assert lib.aur_mha_bwd_ws_bytes(1, 65, 2) == (192 + 2 * 3 * 4096) * 4
     assert lib.aur_mha_kv_ws_bytes(32, 16, 768) >= 32 * 16 * 6 * 66 * 4
+
+
+def test_integration_rust_binding_covers_the_header():
+    """INTEGRATION.md's Rust extern block declares every exported function."""
+    text = (ROOT / "INTEGRATION.md").read_text()
+    missing = [n for n in sorted(declared_functions()) if f"pub fn {n}(" not in text]
+    assert not missing, missing

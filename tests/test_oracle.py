@@ -277,8 +277,8 @@ def test_batch_grads_threads_and_sum_mode():
     cfg = TINY
     P = OM.init_params(cfg, 12)
     rng = np.random.default_rng(12)
-    tok = rng.integers(0, cfg.vocab, (4, 9)).astype(np.uint32)
-    tgt = rng.integers(0, cfg.vocab, (4, 9)).astype(np.uint32)
+    tok = rng.integers(0, cfg.vocab, (4, cfg.seq_len_max)).astype(np.uint32)
+    tgt = rng.integers(0, cfg.vocab, (4, cfg.seq_len_max)).astype(np.uint32)
     l1, G1 = OM.batch_grads(P, cfg, tok, tgt)
     l4, G4 = OM.batch_grads(P, cfg, tok, tgt, threads=4)
     ls, Gs = OM.batch_grads(P, cfg, tok, tgt, threads=3, reduction="sum")
@@ -286,3 +286,12 @@ def test_batch_grads_threads_and_sum_mode():
     for (_, _, a), (_, _, b), (_, _, s) in zip(OM.tensors(G1), OM.tensors(G4), OM.tensors(Gs)):
         assert np.array_equal(a, b)
         np.testing.assert_allclose(s, 4 * a.astype(np.float64), rtol=1e-6, atol=1e-9)
+
+
+def test_embed_refuses_positions_past_the_table():
+    """A sequence longer than w_pos has rows is an error (the reference indexes
+    w_pos[pos] and panics), not an out-of-bounds read."""
+    import oracle as O
+    with pytest.raises(ValueError):
+        O.embed_forward(np.zeros((5, 4), np.float32), np.zeros((3, 4), np.float32),
+                        np.zeros(4, np.uint32), 4)
