@@ -1,4 +1,5 @@
-// Causal multi-head attention on gfx950 fp32 matrix cores, d_head ∈ {8,16,32,64}.
+// Causal multi-head attention on gfx950 fp32 matrix cores, d_head any multiple
+// of 8 up to 64.
 //
 // Reference semantics (src/attention.rs:396-550, src/gpu/attention.rs:21-331):
 //   S = Q_h K_hᵀ / sqrt(d_head), S[i,j] = -inf for j > i, P = softmax_rows(S),
@@ -23,8 +24,8 @@
 // are per-lane scalars and the Sᵀ accumulator registers are directly the
 // B operand of the next product (Oᵀ = Vᵀ·Pᵀ).  The row max is reduced over
 // the four 16-lane groups with cross-lane swizzles (shfl_xor 16, 32).
-// The head dimension is covered in chunks of 16 (NC = ceil(DH/16)); for
-// DH = 8 the upper half of the single chunk is zero.
+// The head dimension is covered in chunks of 16 (NC = ceil(DH/16)); when
+// DH is not a multiple of 16 the last chunk's upper half (8 columns) is zero.
 #include "common.hpp"
 
 #include <cstdlib>
@@ -401,17 +402,20 @@ __global__ void __launch_bounds__(256, 4) mha_fwd_direct_kernel(AttnArgs a) {
 
 // ------------------------------------------------- backward pass 1: rowdot
 // D[b,h,i] = Σ_c dO[i,c]·O[i,c]  (= Σ_j P_ij dP_ij of the reference's fused
-// dscores pass, src/gpu/attention.rs:163-247).  DH/4 lanes per (row, head).
+// dscores pass, src/gpu/attention.rs:163-247).  One lane per float4 of the
+// row, in groups of the next power of two ≥ DH/4 (the surplus lanes add 0).
+constexpr int pow2_at_least(int n) { return n <= 1 ? 1 : 2 * pow2_at_least((n + 1) / 2); }
+
 template <int DH>
 __global__ void __launch_bounds__(256) mha_bwd_rowdot_kernel(AttnArgs a, int B) {
-  constexpr int LPR = DH / 4;            // lanes per row
-  constexpr int RPB = 256 / LPR;         // rows per block
+  constexpr int LPR = pow2_at_least(DH / 4);  // lanes per row
+  constexpr int RPB = 256 / LPR;              // rows per block
   const int gid = blockIdx.x * RPB + threadIdx.x / LPR;  // (b, t, h) flattened
   const int part = threadIdx.x % LPR;
   const int total = B * a.T * a.H;
   float s = 0.f;
   int h = 0, bt = 0;
-  if (gid < total) {
+  if (gid < total && part < DH / 4) {
     h = gid % a.H;
     bt = gid / a.H;
     const floatx4 o = *reinterpret_cast<const floatx4*>(a.o + (size_t)bt * a.ld_o + h * DH + 4 * part);
@@ -421,6 +425,8 @@ __global__ void __launch_bounds__(256) mha_bwd_rowdot_kernel(AttnArgs a, int B) 
 #pragma unroll
   for (int m = LPR / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
   if (gid < total && part == 0) {
+    h = gid % a.H;
+    bt = gid / a.H;
     const int b = bt / a.T, t = bt % a.T;
     a.D[((size_t)b * a.H + h) * a.T + t] = s;
   }
@@ -655,12 +661,13 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 // Workspace: rowdot D [B,H,T], padded to 256 bytes, then the dS tiles.
 size_t ws_d_floats(size_t b, size_t t, size_t n_head) { return (b * t * n_head + 63) / 64 * 64; }
 
-bool dh_supported(uint32_t d) { return d == 8 || d == 16 || d == 32 || d == 64; }
+bool dh_supported(uint32_t d) { return d >= 8 && d <= 64 && d % 8 == 0; }
 
 int check_common(aur_ctx* ctx, uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head,
                  uint32_t ld_qkv, uint32_t ld_o) {
   if (!dh_supported(d_head))
-    return aur::set_error(ctx, AUR_ELIMIT, "attention: d_head=%u, kernels support 8/16/32/64", d_head);
+    return aur::set_error(ctx, AUR_ELIMIT, "attention: d_head=%u, kernels support multiples of 8 up to 64",
+                          d_head);
   if (b == 0 || t == 0 || n_head == 0) return aur::set_error(ctx, AUR_EINVAL, "attention: empty shape");
   if (ld_qkv < n_head * d_head || ld_o < n_head * d_head || (ld_qkv & 3) || (ld_o & 3))
     return aur::set_error(ctx, AUR_EINVAL, "attention: bad row stride (%u, %u)", ld_qkv, ld_o);
@@ -763,7 +770,7 @@ void launch_fwd(const AttnArgs& a, int b, hipStream_t st) {
 
 template <int DH>
 void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
-  constexpr int RPB = 256 / (DH / 4);
+  constexpr int RPB = 256 / pow2_at_least(DH / 4);  // rows per block of mha_bwd_rowdot_kernel
   const size_t rows = (size_t)b * a.T * a.H;
   hipLaunchKernelGGL(mha_bwd_rowdot_kernel<DH>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256),
                      0, st, a, b);
@@ -807,7 +814,11 @@ static int mha_bwd_impl(aur_ctx* ctx, int overwrite, const float* q, const float
   switch (d_head) {
     case 8: launch_bwd<8>(a, (int)b, ctx->stream); break;
     case 16: launch_bwd<16>(a, (int)b, ctx->stream); break;
+    case 24: launch_bwd<24>(a, (int)b, ctx->stream); break;
     case 32: launch_bwd<32>(a, (int)b, ctx->stream); break;
+    case 40: launch_bwd<40>(a, (int)b, ctx->stream); break;
+    case 48: launch_bwd<48>(a, (int)b, ctx->stream); break;
+    case 56: launch_bwd<56>(a, (int)b, ctx->stream); break;
     default: launch_bwd<64>(a, (int)b, ctx->stream); break;
   }
   AUR_LAUNCH_CHECK(ctx, "mha_bwd kernels");
@@ -833,7 +844,11 @@ int aur_mha_fwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v,
   switch (d_head) {
     case 8: launch_fwd<8>(a, (int)b, ctx->stream); break;
     case 16: launch_fwd<16>(a, (int)b, ctx->stream); break;
+    case 24: launch_fwd<24>(a, (int)b, ctx->stream); break;
     case 32: launch_fwd<32>(a, (int)b, ctx->stream); break;
+    case 40: launch_fwd<40>(a, (int)b, ctx->stream); break;
+    case 48: launch_fwd<48>(a, (int)b, ctx->stream); break;
+    case 56: launch_fwd<56>(a, (int)b, ctx->stream); break;
     default: launch_fwd<64>(a, (int)b, ctx->stream); break;
   }
   AUR_LAUNCH_CHECK(ctx, "mha_fwd_kernel");

@@ -9,7 +9,10 @@
 //   * the key axis is split into chunks of KC keys; one 256-thread block per
 //     (chunk, head, sequence) — thousands of blocks at the decode shapes;
 //   * d_head/4 lanes cover one K/V row of a head with float4 loads (256
-//     contiguous bytes at d_head = 64, 4 keys per wave load instruction);
+//     contiguous bytes at d_head = 64, 4 keys per wave load instruction),
+//     in lane groups of the next power of two (d_head = 24, 40, 48, 56 leave
+//     the surplus lanes of a group idle: they read an in-range float4 and
+//     contribute zeros);
 //   * each block writes its chunk's (row max, row sum, unnormalised output);
 //     a second kernel merges the chunks of a (sequence, head) in increasing
 //     chunk order — a fixed order, so the result is deterministic.
@@ -27,6 +30,7 @@
 namespace {
 
 constexpr int DHMAX = 64;
+constexpr int pow2_at_least(int n) { return n <= 1 ? 1 : 2 * pow2_at_least((n + 1) / 2); }
 constexpr int KC = 128;              // keys per chunk (block)
 constexpr int KPW = KC / 4;          // keys per wave
 constexpr int PART = 4 + DHMAX;      // per-chunk record: m, l, pad, pad, o[d_head]
@@ -92,12 +96,14 @@ __device__ __forceinline__ void merge_chunks(const KvArgs& a, int b, int h, int 
 // KPS = 64/LPK keys.
 template <int DH>
 __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
-  constexpr int LPK = DH / 4, KPS = 64 / LPK;
+  constexpr int NP = DH / 4, LPK = pow2_at_least(NP), KPS = 64 / LPK;
   __shared__ float sc[KC];
   __shared__ float red[4];
   __shared__ __attribute__((aligned(16))) float obuf[4][DH];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane / LPK, part = lane % LPK;
+  const bool live = part < NP;             // a lane of the group past the row is idle
+  const int pa = live ? part : NP - 1;     // its loads stay in range
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int T = a.t_dev ? a.t_dev[b] : a.t_scalar;
   const int c0 = c * KC;
@@ -106,8 +112,8 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
     if (tid < PART) rec[tid] = tid == 0 ? -INFINITY : 0.f;
   } else {
     const size_t hist = (size_t)b * a.max_len;
-    floatx4 qv = sum_parts(a.q + (size_t)b * a.ld_q + h * DH + 4 * part, a.nparts, a.pstride);
-    qv *= a.scale * LOG2E;
+    floatx4 qv = sum_parts(a.q + (size_t)b * a.ld_q + h * DH + 4 * pa, a.nparts, a.pstride);
+    qv *= live ? a.scale * LOG2E : 0.f;
 
     // Every K and V row of this wave's keys is requested before any math, so
     // the block has its whole 2·KC·DH·4-byte share of HBM traffic in flight.
@@ -118,14 +124,16 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
       floatx4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
       if (key < T) {
         if (a.knew && key == T - 1) {
-          const size_t o = (size_t)b * a.ld_q + h * DH + 4 * part;
+          const size_t o = (size_t)b * a.ld_q + h * DH + 4 * pa;
           kv = sum_parts(a.knew + o, a.nparts, a.pstride);
           vv = sum_parts(a.vnew + o, a.nparts, a.pstride);
-          *reinterpret_cast<floatx4*>(const_cast<float*>(a.kh) + (hist + key) * a.ld + h * DH + 4 * part) = kv;
-          *reinterpret_cast<floatx4*>(const_cast<float*>(a.vh) + (hist + key) * a.ld + h * DH + 4 * part) = vv;
+          if (live) {
+            *reinterpret_cast<floatx4*>(const_cast<float*>(a.kh) + (hist + key) * a.ld + h * DH + 4 * pa) = kv;
+            *reinterpret_cast<floatx4*>(const_cast<float*>(a.vh) + (hist + key) * a.ld + h * DH + 4 * pa) = vv;
+          }
         } else {
-          kv = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + h * DH + 4 * part);
-          vv = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + h * DH + 4 * part);
+          kv = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + h * DH + 4 * pa);
+          vv = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + h * DH + 4 * pa);
         }
       }
       kreg[it] = kv;
@@ -177,7 +185,7 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int m = LPK; m < 64; m <<= 1) acc[i] += shfl_xor(acc[i], m);
-    if (g == 0) *reinterpret_cast<floatx4*>(&obuf[w][4 * part]) = acc;
+    if (g == 0 && live) *reinterpret_cast<floatx4*>(&obuf[w][4 * part]) = acc;
     __syncthreads();
     if (tid < DH) {
       rec[4 + tid] = (obuf[0][tid] + obuf[1][tid]) + (obuf[2][tid] + obuf[3][tid]);
@@ -199,21 +207,23 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
 constexpr int SW = 8;  // waves per block
 template <int DH, int U>
 __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
-  constexpr int LPK = DH / 4, KPS = 64 / LPK;
+  constexpr int NP = DH / 4, LPK = pow2_at_least(NP), KPS = 64 / LPK;
   constexpr int ROUND = SW * U * KPS;
   __shared__ float wm[SW], wl[SW];
   __shared__ __attribute__((aligned(16))) float wo[SW][DH];
   __shared__ __attribute__((aligned(16))) float qkn[3][DH];  // q (scaled), new k, new v of this head
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane / LPK, part = lane % LPK;
+  const bool live = part < NP;          // a lane of the group past the row is idle
+  const int pa = live ? part : NP - 1;  // its loads stay in range
   const int h = blockIdx.x, b = blockIdx.y;
   const int T = min(a.t_dev ? a.t_dev[b] : a.t_scalar, t_max);
   const size_t hist = (size_t)b * a.max_len;
-  const size_t col = (size_t)h * DH + 4 * part;
+  const size_t col = (size_t)h * DH + 4 * pa;
   // One lane group reads q and the new K/V row (summing the QKV partials)
   // and shares them through LDS; it also appends the new row (position
   // T-1) to the history, which nothing in this launch reads back.
-  if (w == 0 && g == 0) {
+  if (w == 0 && g == 0 && live) {
     const size_t o = (size_t)b * a.ld_q + col;
     const floatx4 q4 = sum_parts(a.q + o, a.nparts, a.pstride) * (a.scale * LOG2E);
     *reinterpret_cast<floatx4*>(&qkn[0][4 * part]) = q4;
@@ -244,11 +254,11 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
   floatx4 kc[U], vc[U];
   load(0, kc, vc);
   __syncthreads();
-  const floatx4 qv = *reinterpret_cast<const floatx4*>(&qkn[0][4 * part]);
+  const floatx4 qv = *reinterpret_cast<const floatx4*>(&qkn[0][4 * pa]) * (live ? 1.f : 0.f);
   floatx4 knew_v = {0.f, 0.f, 0.f, 0.f}, vnew_v = {0.f, 0.f, 0.f, 0.f};
   if (a.knew) {
-    knew_v = *reinterpret_cast<const floatx4*>(&qkn[1][4 * part]);
-    vnew_v = *reinterpret_cast<const floatx4*>(&qkn[2][4 * part]);
+    knew_v = *reinterpret_cast<const floatx4*>(&qkn[1][4 * pa]);
+    vnew_v = *reinterpret_cast<const floatx4*>(&qkn[2][4 * pa]);
   }
   for (int base = 0; base < T; base += ROUND) {
     floatx4 kn[U], vn[U];
@@ -300,7 +310,7 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] += shfl_xor(acc[i], o);
   }
-  if (g == 0) *reinterpret_cast<floatx4*>(&wo[w][4 * part]) = acc;
+  if (g == 0 && live) *reinterpret_cast<floatx4*>(&wo[w][4 * part]) = acc;
   if (lane == 0) {
     wm[w] = m;
     wl[w] = l;
@@ -352,17 +362,24 @@ int launch(aur_ctx* ctx, KvArgs& a, int B, int t_max, int d_head) {
   a.nch = (t_max + KC - 1) / KC;
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   const bool seq = (long)B * a.H >= cus && std::getenv("AUR_KV_CHUNKED") == nullptr;
+#define AUR_KV_CASE(DH) \
+  case DH: seq ? launch_seq<DH>(a, B, t_max, ctx->stream) : launch_dh<DH>(a, B, ctx->stream); break
   switch (d_head) {
-    case 8: seq ? launch_seq<8>(a, B, t_max, ctx->stream) : launch_dh<8>(a, B, ctx->stream); break;
-    case 16: seq ? launch_seq<16>(a, B, t_max, ctx->stream) : launch_dh<16>(a, B, ctx->stream); break;
-    case 32: seq ? launch_seq<32>(a, B, t_max, ctx->stream) : launch_dh<32>(a, B, ctx->stream); break;
+    AUR_KV_CASE(8);
+    AUR_KV_CASE(16);
+    AUR_KV_CASE(24);
+    AUR_KV_CASE(32);
+    AUR_KV_CASE(40);
+    AUR_KV_CASE(48);
+    AUR_KV_CASE(56);
     default: seq ? launch_seq<64>(a, B, t_max, ctx->stream) : launch_dh<64>(a, B, ctx->stream); break;
   }
+#undef AUR_KV_CASE
   AUR_LAUNCH_CHECK(ctx, "kv decode kernels");
   return 0;
 }
 
-bool dh_ok(uint32_t d) { return d == 8 || d == 16 || d == 32 || d == 64; }
+bool dh_ok(uint32_t d) { return d >= 8 && d <= 64 && d % 8 == 0; }
 
 }  // namespace
 
@@ -377,7 +394,7 @@ int aur_mha_kv_step(aur_ctx* ctx, const float* q_new, const float* k_history, co
                     uint32_t max_len) {
   AUR_CHECK_CTX(ctx);
   if (!dh_ok(d_head))
-    return aur::set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%u, supports 8/16/32/64", d_head);
+    return aur::set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%u, supports multiples of 8 up to 64", d_head);
   if (t_total == 0 || t_total > max_len || n_head == 0)
     return aur::set_error(ctx, AUR_EINVAL, "mha_kv_step: t_total=%u max_len=%u", t_total, max_len);
   if (!q_new || !k_history || !v_history || !out || !scratch)
@@ -408,7 +425,7 @@ int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_histor
                    int b, int n_head, int d_head, int max_len, const float* k_new, const float* v_new,
                    int nparts, size_t part_stride) {
   if (!dh_ok((uint32_t)d_head))
-    return set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%d, supports 8/16/32/64", d_head);
+    return set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%d, supports multiples of 8 up to 64", d_head);
   if (b <= 0 || n_head <= 0 || t_max <= 0 || t_max > max_len || ld_q < n_head * d_head || (ld_q & 3))
     return set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: b=%d t_max=%d max_len=%d ld_q=%d", b, t_max,
                      max_len, ld_q);

@@ -110,8 +110,8 @@ DecoderTransformerGpu::DecoderTransformerGpu(aur_ctx* ctx, const TransformerConf
       d % cfg.n_head != 0)
     throw Error("DecoderTransformerGpu: invalid config", AUR_EINVAL);
   const uint32_t dh = cfg.d_model / cfg.n_head;
-  if (!(dh == 8 || dh == 16 || dh == 32 || dh == 64))
-    throw Error("DecoderTransformerGpu: d_head must be 8, 16, 32 or 64", AUR_ELIMIT);
+  if (dh % 8 != 0 || dh > 64)
+    throw Error("DecoderTransformerGpu: d_head must be a multiple of 8 up to 64", AUR_ELIMIT);
   if (d % 4 != 0 || F % 4 != 0 || V % 4 != 0)
     throw Error("DecoderTransformerGpu: vocab, d_model, d_ff must be multiples of 4", AUR_EINVAL);
   // Flat parameter layout: weight-decayed tensors first (w_tok, then per

@@ -132,7 +132,7 @@ int aur_gemm_ex(aur_ctx* ctx, int a_kcontig, int b_kcontig,
  * reads back (it is only the forward→backward hand-off).
  * Replaces CausalMhaForwardKernel::dispatch_into(ctx, enc, q, k, v, out,
  * probs, t, n_head, d_head) (src/gpu/attention.rs:400-443).
- * Limits: d_head ∈ {8, 16, 32, 64} (AUR_ELIMIT otherwise); any t >= 1;
+ * Limits: d_head a multiple of 8 up to 64 (AUR_ELIMIT otherwise); any t >= 1;
  * q/k/v/out 16-byte aligned. */
 int aur_mha_fwd(aur_ctx* ctx, const float* q, const float* k, const float* v,
                 float* out, float* lse,

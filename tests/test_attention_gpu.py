@@ -53,7 +53,8 @@ def _bwd(ctx, q, k, v, o, lse, d_out, B, T, H, dh, init=None):
     return res
 
 
-@pytest.mark.parametrize("t,H,dh", [(4, 2, 8), (8, 4, 16), (12, 2, 32), (70, 2, 64), (129, 3, 32)])
+@pytest.mark.parametrize("t,H,dh", [(4, 2, 8), (8, 4, 16), (12, 2, 32), (70, 2, 64), (129, 3, 32),
+                                    (33, 2, 24), (70, 3, 40), (65, 2, 48), (100, 2, 56)])
 def test_causal_mha_forward_matches_cpu(ctx, t, H, dh):
     rng = np.random.default_rng(0x4274 + t)
     d = H * dh
@@ -66,9 +67,13 @@ def test_causal_mha_forward_matches_cpu(ctx, t, H, dh):
     np.testing.assert_allclose(lse.reshape(1, H, t), l64, rtol=0, atol=1e-4)
 
 
-@pytest.mark.parametrize("t,H,dh", [(6, 2, 8), (12, 2, 32), (65, 2, 64), (200, 1, 16)])
+@pytest.mark.parametrize("t,H,dh", [(6, 2, 8), (12, 2, 32), (65, 2, 64), (200, 1, 16),
+                                    (33, 2, 24), (90, 1, 40), (70, 2, 48), (65, 2, 56)])
 def test_causal_mha_backward_matches_cpu(ctx, t, H, dh):
-    """gpu_parity.rs:267-355: dq/dk/dv accumulate into zeroed buffers."""
+    """gpu_parity.rs:267-355: dq/dk/dv accumulate into zeroed buffers.  The
+    reference's kernels take any d_head ≤ 64 (src/gpu/attention.rs:249-331);
+    here every multiple of 8 is covered, 24/40/48/56 with their last 16-wide
+    head chunk half empty."""
     rng = np.random.default_rng(0x5151 + t)
     d = H * dh
     q, k, v, do = (_n(rng, t * d) for _ in range(4))
@@ -189,7 +194,8 @@ def _kv_single(ctx, q_new, kh, vh, t_total, H, dh, max_len):
 
 
 @pytest.mark.parametrize("t_total,H,dh", [(1, 2, 16), (5, 2, 16), (64, 2, 32), (80, 2, 16),
-                                          (129, 4, 64), (300, 1, 8), (513, 16, 64)])
+                                          (129, 4, 64), (300, 1, 8), (513, 16, 64),
+                                          (100, 2, 24), (70, 2, 40), (129, 3, 48), (65, 2, 56)])
 def test_mha_kv_step_matches_cpu(ctx, t_total, H, dh):
     """tests/kv_cache.rs:346-386 covers t_total=80 > 64 (stride loops)."""
     rng = np.random.default_rng(100 + t_total)
@@ -237,7 +243,7 @@ def test_kv_step_batched_ragged_lengths(ctx):
         assert fro_rel(got[i], want) < TOL_ATTN, i
 
 
-@pytest.mark.parametrize("dh", [8, 16, 32, 64])
+@pytest.mark.parametrize("dh", [8, 16, 24, 32, 40, 48, 56, 64])
 def test_kv_step_batched_one_block_per_head(ctx, dh, monkeypatch):
     """B·H ≥ CU count takes the single-launch path (a block per sequence and
     head, waves merged in LDS).  Ragged lengths including 1 and max_len,

@@ -117,6 +117,25 @@ def test_train_step_wide_rows_matches_cpu(ctx, d, B, T):
     m.destroy()
 
 
+@pytest.mark.parametrize("dh", [24, 40, 48, 56])
+def test_train_step_head_widths_match_cpu(ctx, dh):
+    """d_head values that are multiples of 8 but not of 16 (the reference
+    takes any d_head ≤ 64): one train step over 2 × 70 rows against the
+    oracle, every gradient."""
+    H = 4
+    cfg = OM.Config(vocab=128, d_model=H * dh, n_layer=1, n_head=H, d_ff=2 * H * dh, seq_len_max=80)
+    P = OM.init_params(cfg, 7)
+    tok, tgt = _tokens(cfg, 2, 70, 7)
+    m = _gpu_model(ctx, cfg, 2, P)
+    m.zero_grad()
+    loss_gpu = m.train_step_batch(tok, tgt)
+    loss_cpu, G = OM.batch_grads(P, cfg, tok, tgt)
+    assert abs(loss_gpu - loss_cpu) < 1e-4 * abs(loss_cpu), (loss_gpu, loss_cpu)
+    worst = _compare_tree(m.read_tensors(grad=True), G, 1e-3, "grad")
+    print(f"[d_head {dh}] loss gpu {loss_gpu:.6f} cpu {loss_cpu:.6f} |grad err| <= {worst:.2e}")
+    m.destroy()
+
+
 def test_fused_layernorm_backward_equals_unfused(ctx, monkeypatch):
     """d_model 1024 over 2 × 100 rows (seven 32-row chunks, the last one
     partial): the fused LayerNorm backward gives the gradients of the
@@ -325,12 +344,14 @@ def test_kv_decode_matches_cpu_generate_step(ctx):
     m.destroy()
 
 
-@pytest.mark.parametrize("d,H,F", [(384, 6, 1536), (768, 12, 3072), (640, 10, 2560)])
+@pytest.mark.parametrize("d,H,F", [(384, 6, 1536), (768, 12, 3072), (640, 10, 2560), (384, 8, 1536),
+                                   (96, 4, 192)])
 def test_kv_decode_widths_match_cpu(ctx, d, H, F):
     """Decode at the reference's TransformerConfig::nano width (d 384, H 6,
     d_ff 1536; src/transformer/model.rs:87-96) and at d 768 / 640: K = 384,
     768, 1536, 2560, 3072 give split counts whose K ranges must all be
-    non-empty (the W_o / W_proj partial products)."""
+    non-empty (the W_o / W_proj partial products); d 384 with 8 heads and
+    d 96 with 4 give d_head 48 and 24."""
     cfg = OM.Config(vocab=96, d_model=d, n_layer=2, n_head=H, d_ff=F, seq_len_max=48)
     P = OM.init_params(cfg, 17)
     B, T0, steps = 2, 20, 4
