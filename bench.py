@@ -13,7 +13,9 @@ Prints ONE JSON line (the driver's contract) with a `roofline` object for
 the dominant kernel (the tied-head GEMM launch, timed with HIP events on
 the library's stream) and a `cpu_baseline` object: the reference CPU path's
 GEMM (its linear_forward, restated in oracle/) timed on this host's cores on
-a bounded sample of the same workload.
+a bounded sample of the same workload, with the host (nproc, affinity, CPU
+model), the same GEMM on one thread, a config-2 attention sample, a
+config-4 decode sample and one whole measured config-3 training step.
 """
 from __future__ import annotations
 
@@ -329,101 +331,160 @@ def bench_attention(ctx, steps: int) -> dict:
             "bwd_tflops": round(tf_b, 2), "config": "B16 H8 T1024 dh64 causal fp32"}
 
 
-def cpu_baseline(budget_s: float = 10.0) -> dict:
+CPU_SHARE = 16  # host cores that one GPU's jobs may use on this pool (its worker-pool bound)
+
+
+def cpu_host() -> dict:
+    """The host the CPU legs run on, and the threads they use: all cores of
+    one GPU's CPU share (min(16, affinity)), one sequence per thread as the
+    reference's rayon loops over a batch (examples/aurora_train.rs:828-838)."""
+    aff = len(os.sched_getaffinity(0))
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": aff, "cpu_model": model, "threads": min(CPU_SHARE, aff),
+            "note": f"threads = min({CPU_SHARE}, affinity): one GPU's CPU share on this pool is {CPU_SHARE} cores"}
+
+
+def cpu_baseline(threads: int, budget_s: float = 10.0) -> dict:
     """The reference CPU path's GEMM: linear_forward (src/attention.rs:219-238)
-    restated in oracle/, one 64-row "sequence" per task over a thread pool as
-    the reference's rayon loop does, on the sweep's QKV shape
-    [rows,512]·[1536,512]ᵀ until `budget_s` of wall time is used."""
+    restated in oracle/, one 64-row "sequence" per task over `threads`
+    threads as the reference's rayon loop does, on the sweep's QKV shape
+    [rows,512]·[1536,512]ᵀ until `budget_s` of wall time is used; then the
+    same GEMM on one thread for a fifth of the budget."""
     import oracle
 
-    threads = min(16, len(os.sched_getaffinity(0)))
     rng = np.random.default_rng(0)
     k, n, rows = 512, 1536, 1024
     x = rng.uniform(-1, 1, rows * k).astype(np.float32)
     w = rng.uniform(-1, 1, n * k).astype(np.float32)
-    oracle.linear_forward_seqs(w, x, k, n, 64, threads)  # warm-up
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        oracle.linear_forward_seqs(w, x, k, n, 64, threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    tflops = 2.0 * rows * k * n * reps / el / 1e12
-    return {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+
+    def rate(nthreads, budget):
+        oracle.linear_forward_seqs(w, x, k, n, 64, nthreads)  # warm-up
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            oracle.linear_forward_seqs(w, x, k, n, 64, nthreads)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return 2.0 * rows * k * n * reps / el / 1e12, reps, el
+
+    tf, reps, el = rate(threads, budget_s)
+    tf1, reps1, el1 = rate(1, budget_s / 5)
+    return {"value": round(tf, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"linear_forward [{rows},512]x[1536,512]^T (the sweep's QKV GEMM, "
-                      f"1/8 of its rows) x{reps} in {el:.1f}s, 64-row sequences over {threads} threads"}
+                      f"1/8 of its rows) x{reps} in {el:.1f}s, 64-row sequences over {threads} threads",
+            "gemm_1thread_tflops": round(tf1, 5),
+            "gemm_1thread_sample": f"the same GEMM x{reps1} in {el1:.1f}s on one thread"}
 
 
-def cpu_decode_sample(n_steps: int = 6) -> dict:
+def cpu_attention_sample(threads: int) -> dict:
+    """Config 2 on the reference CPU path: scaled_dot_product_attention and
+    its backward (src/attention.rs:396-550, restated in oracle/) for one
+    (sequence, head) — T 1024, d_head 64, causal — one per thread on `threads`
+    threads at once, timed; the 128 (b, h) pairs of config 2 take
+    128 / threads such rounds."""
+    import oracle
+    from concurrent.futures import ThreadPoolExecutor
+
+    T, dh = 1024, 64
+    rng = np.random.default_rng(1)
+    heads = [tuple(rng.standard_normal(T * dh, dtype=np.float32) for _ in range(4)) for _ in range(threads)]
+
+    def one(h):
+        q, k, v, do = h
+        out, probs = oracle.sdpa_forward(q, k, v, dh, dh, causal=True)
+        oracle.sdpa_backward(q, k, v, probs, do, dh, dh)
+
+    one(heads[0])  # warm-up
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(one, heads))
+        el = time.perf_counter() - t0
+    rounds = (16 * 8 + threads - 1) // threads
+    return {"s_per_round": round(el, 3), "threads": threads, "c2_fwd_bwd_s_est": round(el * rounds, 2),
+            "sample": f"oracle sdpa forward + backward, one (sequence, head) of T 1024 d_head 64 per thread, "
+                      f"{threads} at once in {el:.2f}s; config 2 (B16 x H8 = 128 heads) = {rounds} such rounds"}
+
+
+def cpu_decode_sample(threads: int, n_steps: int = 4) -> dict:
     """The reference CPU decode path (kv_cache.rs generate_step, restated in
-    oracle/model.py) on the config-4 model for ONE sequence, single-threaded,
+    oracle/model.py) on the config-4 model: `threads` sequences decoded at
+    once, one per thread (the reference runs sequences in parallel), each
     with its KV cache pre-filled to 640 positions (the average length of the
-    256-step C4 run; the step's cost does not depend on the cached values).
-    The reference runs the 32 sequences in parallel over the host's cores
-    (rayon), so tok/s at C cores ≈ C / (seconds per step)."""
+    256-step config-4 run), n_steps greedy steps each, timed."""
+    from concurrent.futures import ThreadPoolExecutor
+
     from oracle import model as om
 
     cfg = om.Config(vocab=C3["vocab"], d_model=C3["d_model"], n_layer=C3["n_layer"], n_head=C3["n_head"],
                     d_ff=C3["d_ff"], seq_len_max=768 + 64)
     P = om.init_params(cfg, 2)
     rng = np.random.default_rng(5)
-    kv = om.KvCache(cfg)
     t0 = 640
-    for l in range(cfg.n_layer):
-        kv.k[l] = rng.standard_normal(t0 * cfg.d_model, dtype=np.float32)
-        kv.v[l] = rng.standard_normal(t0 * cfg.d_model, dtype=np.float32)
-    kv.current_len = t0
-    tok = 17
-    om.generate_step(P, cfg, kv, tok)  # warm-up
-    t_start = time.perf_counter()
-    for _ in range(n_steps):
-        tok = om.argmax(om.generate_step(P, cfg, kv, tok))
-    sec = (time.perf_counter() - t_start) / n_steps
-    cores = min(16, len(os.sched_getaffinity(0)))
-    return {"s_per_token_1core": round(sec, 4), "cores": cores, "tok_per_s_est": round(cores / sec, 1),
-            "sample": f"oracle generate_step, config-4 model, one sequence at KV length {t0}..{t0 + n_steps}, "
-                      f"{n_steps} steps single-threaded; tok_per_s_est = cores / s_per_token (the reference "
-                      f"decodes sequences in parallel)"}
+    caches = []
+    for _ in range(threads):
+        kv = om.KvCache(cfg)
+        for l in range(cfg.n_layer):
+            kv.k[l] = rng.standard_normal(t0 * cfg.d_model, dtype=np.float32)
+            kv.v[l] = rng.standard_normal(t0 * cfg.d_model, dtype=np.float32)
+        kv.current_len = t0
+        caches.append(kv)
+
+    def run(kv, steps):
+        tok = 17
+        for _ in range(steps):
+            tok = om.argmax(om.generate_step(P, cfg, kv, tok))
+
+    run(caches[0], 1)  # warm-up (one sequence one step longer)
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        ts = time.perf_counter()
+        list(ex.map(lambda kv: run(kv, n_steps), caches))
+        el = time.perf_counter() - ts
+    tok_s = threads * n_steps / el
+    return {"tok_per_s": round(tok_s, 1), "threads": threads, "s_per_step": round(el / n_steps, 4),
+            "sample": f"oracle generate_step, config-4 model, {threads} sequences at once (one per thread) at KV "
+                      f"length {t0}..{t0 + n_steps}, {n_steps} greedy steps each in {el:.2f}s"}
 
 
-def cpu_train_sample(t: int = 32) -> dict:
-    """The reference CPU training path (forward, CE, backward, clip, AdamW —
-    oracle/model.py restating model.rs / optimizer.rs) on the config-3 model
-    for ONE sequence of t tokens, single-threaded, timed once after a warm-up.
-    The reference computes a batch's per-sequence gradients in parallel
-    (rayon), so a config-3 step (16 × 1024 tokens) over C cores is estimated
-    as forward+backward per token × 16384 / C × (1 + 0.09) — the linear and
-    head FLOP scale with tokens, causal attention adds 1.44 of 15.67 TFLOP at
-    T = 1024 (≈ 0 at t) — plus the clip + AdamW pass once."""
+def cpu_train_step(threads: int, full: bool = True) -> dict:
+    """The reference CPU training path on config 3 (model.rs forward, CE,
+    backward; aurora_train.rs:812-848 batch loop; clip 1.0; AdamW): one whole
+    step of 16 sequences × 1024 tokens, the sequences' gradients computed
+    `threads` at a time (one per thread, as rayon par_iter over the batch),
+    summed in sequence order and scaled by 1/16, then clip + AdamW — timed
+    once, measured, no extrapolation.  full=False times one 32-token
+    sequence instead (a quick sample for profiling runs)."""
     from oracle import model as om
 
     cfg = om.Config(vocab=C3["vocab"], d_model=C3["d_model"], n_layer=C3["n_layer"], n_head=C3["n_head"],
                     d_ff=C3["d_ff"], seq_len_max=C3["seq_len_max"])
     P = om.init_params(cfg, 2)
-    rng = np.random.default_rng(6)
-    seq = rng.integers(0, cfg.vocab, (1, t + 1)).astype(np.uint32)
-    tok, tgt = seq[:, :t], seq[:, 1:]
+    B, T = (16, 1024) if full else (1, 32)
+    seq = np.random.default_rng(2).integers(0, cfg.vocab, (B, T + 1)).astype(np.uint32)
     state = om.new_adam_state(P)
-
-    def step():
-        t0 = time.perf_counter()
-        _, G = om.batch_grads(P, cfg, tok, tgt)
-        t1 = time.perf_counter()
-        om.clip_grads(G, 1.0)
-        om.step_adamw(P, G, state, lr=3e-4, wd=0.1)
-        return t1 - t0, time.perf_counter() - t1
-
-    step()
-    fb, opt = step()
-    cores = min(16, len(os.sched_getaffinity(0)))
-    est = fb / t * 16 * 1024 / cores * (1.0 + 1.44 / 15.67) + opt
-    return {"s_fwd_bwd_one_seq": round(fb, 3), "s_clip_adamw": round(opt, 3), "tokens": t, "cores": cores,
-            "c3_step_s_est": round(est, 1),
-            "sample": f"oracle batch_grads, then clip + AdamW, config-3 model, one sequence of {t} tokens, "
-                      f"single-threaded; c3_step_s_est = forward+backward per token x 16 x 1024 tokens over "
-                      f"the cores (+9 % causal attention at T = 1024) + clip + AdamW once"}
+    t0 = time.perf_counter()
+    loss, G = om.batch_grads(P, cfg, seq[:, :T], seq[:, 1:], threads=threads)
+    t1 = time.perf_counter()
+    om.clip_grads(G, 1.0)
+    om.step_adamw(P, G, state, lr=3e-4, wd=0.1)
+    t2 = time.perf_counter()
+    out = {"s_fwd_bwd": round(t1 - t0, 2), "s_clip_adamw": round(t2 - t1, 2), "threads": threads,
+           "loss": round(loss / B, 4)}
+    if full:
+        out["c3_step_s"] = round(t2 - t0, 2)
+        out["sample"] = (f"oracle batch_grads over the full config-3 batch (16 x 1024 tokens, {threads} sequences "
+                         f"at a time), then clip + AdamW: one measured step")
+    else:
+        out["sample"] = "oracle batch_grads + clip + AdamW on one 32-token sequence (not a config-3 step)"
+    return out
 
 
 def main() -> int:
@@ -436,6 +497,9 @@ def main() -> int:
                     help="profile helper: time only this part and skip the CPU baseline")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--cpu-train", choices=["full", "sample"], default="full",
+                    help="full: time a whole config-3 CPU step (about a minute on 16 cores); "
+                         "sample: one 32-token sequence")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -529,13 +593,24 @@ def main() -> int:
     attn = bench_attention(ctx, max(3, args.steps // 4))
     train = bench_train(ctx, max(2, min(args.steps, 5)), min(args.warmup, 2))
     decode = bench_decode(ctx, args.decode_steps)
-    cpu = cpu_baseline(args.cpu_budget)
-    # The same leg also times the reference CPU decode step (config 4).
-    cpu["decode"] = cpu_decode_sample()
-    cpu["decode"]["gpu_speedup"] = round(decode["tok_per_s"] / cpu["decode"]["tok_per_s_est"], 1)
-    cpu["train"] = cpu_train_sample()
-    cpu["train"]["gpu_speedup"] = round(cpu["train"]["c3_step_s_est"] / (train["ms_per_step"] * 1e-3), 1)
-    log(f"[bench] cpu baseline {cpu}")
+    host = cpu_host()
+    thr = host["threads"]
+    cpu = cpu_baseline(thr, args.cpu_budget)
+    cpu["host"] = host
+    log(f"[bench] cpu gemm {cpu['value']} TFLOP/s on {thr} threads, {cpu['gemm_1thread_tflops']} on one")
+    # The same leg also times the reference CPU attention (config 2), decode
+    # (config 4) and training step (config 3).
+    cpu["attention"] = cpu_attention_sample(thr)
+    cpu["attention"]["gpu_speedup"] = round(
+        cpu["attention"]["c2_fwd_bwd_s_est"] / ((attn["fwd_ms"] + attn["bwd_ms"]) * 1e-3), 1)
+    log(f"[bench] cpu attention {cpu['attention']}")
+    cpu["decode"] = cpu_decode_sample(thr)
+    cpu["decode"]["gpu_speedup"] = round(decode["tok_per_s"] / cpu["decode"]["tok_per_s"], 1)
+    log(f"[bench] cpu decode {cpu['decode']}")
+    cpu["train"] = cpu_train_step(thr, full=args.cpu_train == "full")
+    if "c3_step_s" in cpu["train"]:
+        cpu["train"]["gpu_speedup"] = round(cpu["train"]["c3_step_s"] / (train["ms_per_step"] * 1e-3), 1)
+    log(f"[bench] cpu train {cpu['train']}")
 
     line = {
         "metric": "fp32 GEMM TFLOP/s (% MFMA peak); train tok/s d1024 L12; decode tok/s + GB/s",
