@@ -376,7 +376,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
 //     granule within it);
 //   k-strided operand, [BK][ROWS]: granule q of k-row k at q ^ (((k >> 2) & 3) << 2)
 //     (the four k-rows 4g + s of a b32 fragment read land in 4 different
-//     granule groups).
+//     granule groups); rows of 8 granules (32-row tiles) use q ^ (((k >> 2) & 1) << 2),
+//     two groups, so every granule stays in its row.
 // The swizzle is an involution, so the same function maps physical → logical
 // on the load side.
 template <int ROWS, bool KCONTIG, int BK = 32>
@@ -388,9 +389,13 @@ struct DirectTile {
   static constexpr int NIW = (KCONTIG ? ROWS : BK) / RPI / 4;  // instructions per wave
   static_assert(NIW >= 1 && (KCONTIG ? ROWS : BK) % (RPI * 4) == 0, "tile too small for four waves");
 
+  static_assert(KCONTIG || GPR >= 8, "the k-strided swizzle needs at least 8 granules per LDS row");
   __device__ static __forceinline__ int phys(int lrow, int q) {
     if (KCONTIG) return BK == 32 ? q ^ ((lrow >> 1) & 7) : q ^ ((lrow >> 2) & 3);
-    return q ^ (((lrow >> 2) & 3) << 2);
+    // k-strided rows of 32 floats (8 granules, 32-row tiles) XOR with 0 or 4
+    // only: the wider XOR of 16-granule rows would leave the row (and the
+    // tile: past the end of the operand at its last column tile).
+    return q ^ (((lrow >> 2) & (GPR >= 16 ? 3 : 1)) << 2);
   }
   // This wave's share of the tile at (row origin r0, k origin k0).
   __device__ static __forceinline__ void issue(const float* __restrict__ x, int ld, int r0, int k0,
@@ -861,7 +866,7 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int 
     int bm = 0, bn = 0, sp = 1;
     if (std::sscanf(env, "%dx%d:%d", &bm, &bn, &sp) >= 2 &&
         ((bm == 128 && bn == 128) || (bm == 128 && bn == 64) || (bm == 64 && bn == 64) ||
-         (bm == 256 && bn == 128 && allow_wide))) {
+         (bm == 64 && bn == 32) || (bm == 32 && bn == 32) || (bm == 256 && bn == 128 && allow_wide))) {
       p.bm = bm;
       p.bn = bn;
       if (!allow_split) sp = 1;
@@ -913,8 +918,12 @@ void launch_layout(const GemmArgs& a, const Plan& p, bool vec, hipStream_t st, i
     launch_tile<128, 128, AK, BKC>(a, p.splits, vec, st, batch);
   else if (p.bm == 128 && p.bn == 64)
     launch_tile<128, 64, AK, BKC>(a, p.splits, vec, st, batch);
-  else
+  else if (p.bm == 64 && p.bn == 64)
     launch_tile<64, 64, AK, BKC>(a, p.splits, vec, st, batch);
+  else if (p.bm == 64 && p.bn == 32)
+    launch_tile<64, 32, AK, BKC>(a, p.splits, vec, st, batch);
+  else
+    launch_tile<32, 32, AK, BKC>(a, p.splits, vec, st, batch);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

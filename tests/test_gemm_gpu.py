@@ -148,19 +148,42 @@ def test_seeded_random_shapes_all_forms(ctx, m, k, n):
 
 
 @pytest.mark.parametrize("cfg", ["256x128:1", "256x128:2", "128x128:1", "128x128:4", "128x64:1",
-                                 "128x64:2", "64x64:1", "64x64:4", "staged"])
+                                 "128x64:2", "64x64:1", "64x64:4", "64x32:1", "64x32:4", "32x32:1",
+                                 "32x32:8", "staged"])
 def test_every_tile_config_all_forms(ctx, monkeypatch, cfg):
     """Every kernel variant the planner can pick, forced through the tuning
     override (read on each call), on a whole-tile shape: the 256×128 BK=16
-    tile (A k-contiguous forms), the 128×128 / 128×64 / 64×64 direct-load
-    tiles, split-K 2 and 4 with the ordered reduction, and the register-staged
-    kernel.  All three forms against float64."""
+    tile (A k-contiguous forms), the 128×128 / 128×64 / 64×64 / 64×32 / 32×32
+    direct-load tiles (the 32-row tiles' k-strided operands swizzled within
+    their 32-float rows), split-K 2 to 8 with the ordered reduction, and the
+    register-staged kernel.  All three forms against float64."""
     if cfg == "staged":
         monkeypatch.setenv("AUR_GEMM_STAGED", "1")
     else:
         monkeypatch.setenv("AUR_GEMM_CFG", cfg)
     m, k, n = 512, 2048, 384
     rng = np.random.default_rng(7100 + len(cfg))
+    a = _u(rng, m * k)
+    b_nn, b_nt = _u(rng, k * n), _u(rng, n * k)
+    a64 = a.reshape(m, k).astype(np.float64)
+    cw, fr = _gates(_nn(ctx, a, b_nn, m, n, k), a64, b_nn.reshape(k, n).astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("nn", cfg, cw, fr)
+    cw, fr = _gates(_nt(ctx, a, b_nt, m, n, k), a64, b_nt.reshape(n, k).T.astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("nt", cfg, cw, fr)
+    x, dy, dest = _u(rng, k * n), _u(rng, k * m), _u(rng, m * n)
+    got = _outer(ctx, x, dy, dest, m, n, k)
+    cw, fr = _gates(got, dy.reshape(k, m).T.astype(np.float64), x.reshape(k, n).astype(np.float64),
+                    dest.reshape(m, n))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, ("outer", cfg, cw, fr)
+
+
+@pytest.mark.parametrize("cfg", ["64x32:1", "64x32:2", "32x32:1", "32x32:4"])
+def test_small_tiles_ragged_shapes(ctx, monkeypatch, cfg):
+    """The 64×32 and 32×32 tiles on a ragged shape (the register-staged
+    kernel, partial edge tiles, K not a multiple of 32), all three forms."""
+    monkeypatch.setenv("AUR_GEMM_CFG", cfg)
+    m, k, n = 100, 300, 70
+    rng = np.random.default_rng(7300 + len(cfg))
     a = _u(rng, m * k)
     b_nn, b_nt = _u(rng, k * n), _u(rng, n * k)
     a64 = a.reshape(m, k).astype(np.float64)
