@@ -825,8 +825,8 @@ constexpr int kBK = 32;
 // by aurora_amd/tune_gemm.py: tile efficiency 1.00 / 0.95 / 0.85 / 0.70 /
 // 0.55 (128×128 / 128×64 / 64×64 / 64×32 / 32×32), single-block factor 0.8
 // / 0.7 / 0.7 / 0.7 / 0.7, 3 TB/s for the reduction and 2 µs per launch;
-// the pick is within 2.8 % of the measured best on every shape (0.2 % on
-// average).  The two small tiles serve few-tile shapes (M = 1024 with
+// on the fitting run the pick was within 2.8 % of the measured best on
+// every shape (0.2 % on average).  The two small tiles serve few-tile shapes (M = 1024 with
 // N = 512: 24 → 38 % of peak).
 //
 // allow_wide admits the 256×128 tile (direct-load kernel only: whole tiles,
