@@ -28,6 +28,7 @@
 // DH is not a multiple of 16 the last chunk's upper half (8 columns) is zero.
 #include "common.hpp"
 
+#include <algorithm>
 #include <cstdlib>
 
 namespace {
@@ -537,8 +538,11 @@ __global__ void __launch_bounds__(256, (NS == 1 ? 3 : 1)) mha_bwd_dkv_kernel(Att
         if (qt == kt && krow > q) pe = 0.f;
         p[e] = pe;
         ds[e] = pe * (dp[e] - Dq[e]);
-        // dS tile (qt, kt), row-major [q][key], for the dQ pass
-        ds_tile[(16 * jq + 4 * g + e) * TQ + 16 * w + l16] = ds[e];
+        // dS tile (qt, kt), row-major [q][key], for the dQ pass.  Streamed
+        // (non-temporal): it is read back only after the whole pass, and
+        // keeping it out of L2 leaves room for the Q / dO tiles this block
+        // and its neighbours re-read (pass 2 fetches 432 → 279 MB at C2).
+        __builtin_nontemporal_store(ds[e], &ds_tile[(16 * jq + 4 * g + e) * TQ + 16 * w + l16]);
       }
       // dVᵀ[d][key] += dOᵀ[d][q]·P[q][key];  dKᵀ[d][key] += Qᵀ[d][q]·dS[q][key]
 #pragma unroll
@@ -602,9 +606,10 @@ __global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
   // dS tile (qt, kt) at tiles + kt·TQ², this lane's row and column offset folded in
   const float* tiles = a.ds + (((size_t)b * a.H + h) * a.ntri + qt * (qt + 1) / 2) * (TQ * TQ) +
                        (16 * w + l16) * TQ + 4 * g;
-  auto load_ds = [&](int kt, floatx4* f) {
+  auto load_ds = [&](int kt, floatx4* f) {  // read once: streamed past L2
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f[j] = *reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + 16 * j);
+    for (int j = 0; j < 4; ++j)
+      f[j] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + 16 * j));
   };
 
   floatx4 acc[NC];
@@ -696,7 +701,10 @@ __global__ void __launch_bounds__(256, 5) mha_bwd_dq_direct_kernel(AttnArgs a) {
                        (16 * w + l16) * TQ + 4 * g;
   auto load_ds = [&](int kt, floatx4* f) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f[j] = *reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + 16 * j);
+    for (int j = 0; j < 4; ++j) {
+      // read once: streamed past L2, which keeps the K tiles
+      f[j] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + 16 * j));
+    }
   };
   auto issue_k = [&](int kt, float* lds) {
 #pragma unroll

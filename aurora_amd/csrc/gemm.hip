@@ -972,6 +972,12 @@ static int partials(aur_ctx* ctx, const Workspace* ws, size_t floats, float** ou
     *out = ws->ptr;
     return 0;
   }
+  // A graph captured now would keep the context workspace's address, which
+  // a later growth frees: captured split-K work must bring its own.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  AUR_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return set_error(ctx, AUR_EINVAL, "gemm: split-K while the stream is captured needs a Workspace");
   int rc = ensure_workspace(ctx, floats * sizeof(float));
   if (rc) return rc;
   *out = static_cast<float*>(ctx->ws);

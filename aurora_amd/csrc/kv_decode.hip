@@ -220,6 +220,24 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
   const int T = min(a.t_dev ? a.t_dev[b] : a.t_scalar, t_max);
   const size_t hist = (size_t)b * a.max_len;
   const size_t col = (size_t)h * DH + 4 * pa;
+  const int last = max(T - 1, 0);
+  // History rows only: the new row's slot may be mid-append (every value in
+  // it is finite either way); key T-1 takes the shared row before use.
+  auto load = [&](int base, floatx4* kr, floatx4* vr) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = min(base + (u * SW + w) * KPS + g, last);
+      kr[u] = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + col);
+      vr[u] = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + col);
+    }
+  };
+  float m = -INFINITY, l = 0.f;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  floatx4 kc[U], vc[U];
+  // The first round's history loads go out before the QKV-partial loads
+  // below, so the block waits for one memory round trip, not two (the
+  // append's stores would otherwise keep them behind it).
+  load(0, kc, vc);
   // One lane group reads q and the new K/V row (summing the QKV partials)
   // and shares them through LDS; it also appends the new row (position
   // T-1) to the history, which nothing in this launch reads back.
@@ -238,21 +256,6 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
       }
     }
   }
-  const int last = max(T - 1, 0);
-  // History rows only: the new row's slot may be mid-append (every value in
-  // it is finite either way); key T-1 takes the shared row before use.
-  auto load = [&](int base, floatx4* kr, floatx4* vr) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int key = min(base + (u * SW + w) * KPS + g, last);
-      kr[u] = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + col);
-      vr[u] = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + col);
-    }
-  };
-  float m = -INFINITY, l = 0.f;
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  floatx4 kc[U], vc[U];
-  load(0, kc, vc);
   __syncthreads();
   const floatx4 qv = *reinterpret_cast<const floatx4*>(&qkn[0][4 * pa]) * (live ? 1.f : 0.f);
   floatx4 knew_v = {0.f, 0.f, 0.f, 0.f}, vnew_v = {0.f, 0.f, 0.f, 0.f};

@@ -294,3 +294,41 @@ def test_nt_equals_nn_on_materialised_transpose(ctx):
     nt = _nt(ctx, a, b, m, n, k)
     nn = _nn(ctx, a, np.ascontiguousarray(b.reshape(n, k).T).ravel(), m, n, k)
     assert fro_rel(nt, nn) < 1e-6
+
+
+def test_split_k_refused_while_captured(ctx, monkeypatch):
+    """A split-K GEMM enqueued while the library's stream is being captured
+    into a HIP graph, without a caller workspace, is refused (the graph would
+    keep the address of the context's grow-only workspace); nothing is
+    enqueued, and the same call outside the capture runs."""
+    import ctypes
+
+    from aurora_amd._lib import AuroraError, load
+    from aurora_amd.gpu import GpuBuffer
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+    stream = load().aur_stream(ctx.ptr)
+    m, n, k = 128, 128, 4096
+    rng = np.random.default_rng(31)
+    a, b = _u(rng, m * k), _u(rng, n * k)
+    ab, bb, cb = GpuBuffer.from_slice(ctx, a), GpuBuffer.from_slice(ctx, b), GpuBuffer.zeros(ctx, m * n)
+    monkeypatch.setenv("AUR_GEMM_CFG", "64x64:4")
+    ctx.sync()
+    assert hip.hipStreamBeginCapture(stream, 1) == 0  # hipStreamCaptureModeThreadLocal
+    try:
+        with pytest.raises(AuroraError, match="captured"):
+            ctx.call("aur_gemm_nt", ab.ptr, bb.ptr, cb.ptr, m, n, k)
+    finally:
+        g = ctypes.c_void_p()
+        assert hip.hipStreamEndCapture(stream, ctypes.byref(g)) == 0
+        if g.value:
+            hip.hipGraphDestroy(g)
+    ctx.call("aur_gemm_nt", ab.ptr, bb.ptr, cb.ptr, m, n, k)
+    got = cb.download()
+    for x in (ab, bb, cb):
+        x.free()
+    cw, fr = _gates(got, a.reshape(m, k).astype(np.float64), b.reshape(n, k).T.astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
