@@ -17,6 +17,9 @@ CSRC = PKG / "csrc"
 OUT_DIR = PKG / "_build"
 LIB = PKG / "libaurora_hip.so"
 INCLUDE = PKG.parent / "include"
+# Roofline ceiling probes (a measurement aid for bench.py, not the C ABI).
+PROBE_SRC = PKG / "probes" / "ceilings.hip"
+PROBE_LIB = PKG / "libaurora_ceilings.so"
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -64,9 +67,21 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_probes()
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
+        print(f"built {LIB} from {len(srcs)} sources, and {PROBE_LIB.name}")
     return LIB
+
+
+def build_probes() -> Path:
+    """Compile the ceiling probes into their own shared library."""
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, *DEVICE_FLAGS, "-shared", str(PROBE_SRC), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 if __name__ == "__main__":

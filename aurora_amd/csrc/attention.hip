@@ -541,7 +541,9 @@ __global__ void __launch_bounds__(256, (NS == 1 ? 3 : 1)) mha_bwd_dkv_kernel(Att
         // dS tile (qt, kt), row-major [q][key], for the dQ pass.  Streamed
         // (non-temporal): it is read back only after the whole pass, and
         // keeping it out of L2 leaves room for the Q / dO tiles this block
-        // and its neighbours re-read (pass 2 fetches 432 → 279 MB at C2).
+        // and its neighbours re-read (at B16 H8 T1024 this pass fetches
+        // 280-380 MB instead of 432 MB, and writes 432 MB instead of 345:
+        // the two waves' halves of a line are no longer merged in L2).
         __builtin_nontemporal_store(ds[e], &ds_tile[(16 * jq + 4 * g + e) * TQ + 16 * w + l16]);
       }
       // dVᵀ[d][key] += dOᵀ[d][q]·P[q][key];  dKᵀ[d][key] += Qᵀ[d][q]·dS[q][key]

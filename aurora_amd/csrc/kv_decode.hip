@@ -197,15 +197,15 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
   }
 }
 
-// One block of SW waves per (head, sequence).  Round r covers keys
-// [r·SW·U·KPS, (r+1)·SW·U·KPS); wave w loads its U key groups of the round
-// (KPS keys per load instruction, LPK lanes per key) and folds them into its
-// running (m, l, acc) in the log2 domain.  The loads are branch-free (a key
+// One block of SW waves per (head, sequence); NT: the history rows, read
+// once per step, are loaded non-temporally (streamed past the caches).
+// Round r covers keys [r·SW·U·KPS, (r+1)·SW·U·KPS); wave w loads its U key
+// groups of the round (KPS keys per load instruction, LPK lanes per key) and
+// folds them into its running (m, l, acc) in the log2 domain.  The loads are branch-free (a key
 // past the end is clamped to the last one and masked in the math) and the
 // next round is loaded before the current one is used, so each wave keeps
 // two rounds of HBM reads in flight instead of one round trip per round.
-constexpr int SW = 8;  // waves per block
-template <int DH, int U>
+template <int DH, int U, int SW, bool NT>
 __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
   constexpr int NP = DH / 4, LPK = pow2_at_least(NP), KPS = 64 / LPK;
   constexpr int ROUND = SW * U * KPS;
@@ -227,8 +227,10 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int key = min(base + (u * SW + w) * KPS + g, last);
-      kr[u] = *reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + col);
-      vr[u] = *reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + col);
+      const floatx4* kp = reinterpret_cast<const floatx4*>(a.kh + (hist + key) * a.ld + col);
+      const floatx4* vp = reinterpret_cast<const floatx4*>(a.vh + (hist + key) * a.ld + col);
+      kr[u] = NT ? __builtin_nontemporal_load(kp) : *kp;
+      vr[u] = NT ? __builtin_nontemporal_load(vp) : *vp;
     }
   };
   float m = -INFINITY, l = 0.f;
@@ -354,11 +356,15 @@ void launch_dh(const KvArgs& a, int B, hipStream_t st) {
 
 template <int DH>
 void launch_seq(const KvArgs& a, int B, int t_max, hipStream_t st) {
-  // U = 4 key groups per wave per round (four K and four V float4 loads in
-  // flight per lane, twice that with the prefetched round).  Measured on
-  // MI355X inside the decode graph (12 layers' histories, B32 H16 dh64):
-  // U = 2 / 4 → 31.1 / 30.2 µs per layer at T = 640; C4 step 0.889 → 0.874 ms.
-  hipLaunchKernelGGL((kv_seq_kernel<DH, 4>), dim3(a.H, B), dim3(64 * SW), 0, st, a, t_max);
+  // 4 waves per block (two blocks, eight waves per CU at B·H = 512), U = 2
+  // key groups per wave per round, history rows loaded non-temporally.
+  // Measured on MI355X in the config-4 decode step (0.865 ms/step with 8
+  // waves, U = 4, cached loads): non-temporal loads alone 0.831, with 4
+  // waves 0.827, 4 waves and U = 2 0.815; U = 1 0.859, 2 waves 0.879, the
+  // best shape without non-temporal loads 0.864.  A plain 2 GiB read
+  // behaves alike: fastest with two 4-wave blocks per CU and non-temporal
+  // loads (6.5 TB/s; 5.0-5.9 TB/s with more waves per CU or cached loads).
+  hipLaunchKernelGGL((kv_seq_kernel<DH, 2, 4, true>), dim3(a.H, B), dim3(64 * 4), 0, st, a, t_max);
 }
 
 int launch(aur_ctx* ctx, KvArgs& a, int B, int t_max, int d_head) {

@@ -222,6 +222,17 @@ __global__ void __launch_bounds__(256) ln_fwd_sum_kernel(const float* __restrict
                                                          float* __restrict__ y, int d, float eps) {
   __shared__ float red[4];
   const int r = blockIdx.x;
+  // γ and β are requested with the row, not after the two reductions: one
+  // memory round trip fewer per launch.
+  floatx4 gg[4], bb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (threadIdx.x + 256 * i) * 4;
+    if (c < d) {
+      gg[i] = *reinterpret_cast<const floatx4*>(gamma + c);
+      bb[i] = *reinterpret_cast<const floatx4*>(beta + c);
+    }
+  }
   floatx4 xv[4];
   float s = 0.f;
 #pragma unroll
@@ -264,11 +275,9 @@ __global__ void __launch_bounds__(256) ln_fwd_sum_kernel(const float* __restrict
   for (int i = 0; i < 4; ++i) {
     const int c = (threadIdx.x + 256 * i) * 4;
     if (c < d) {
-      const floatx4 gg = *reinterpret_cast<const floatx4*>(gamma + c);
-      const floatx4 bb = *reinterpret_cast<const floatx4*>(beta + c);
       floatx4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (xv[i][e] - mu) * is * gg[e] + bb[e];
+      for (int e = 0; e < 4; ++e) o[e] = (xv[i][e] - mu) * is * gg[i][e] + bb[i][e];
       *reinterpret_cast<floatx4*>(y + (size_t)r * d + c) = o;
     }
   }
@@ -875,6 +884,15 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(const float* __restrict__
                                                        int32_t* __restrict__ lens, int d, float eps) {
   __shared__ float red[4];
   const int r = blockIdx.x;
+  floatx4 gg[4], bb[4];  // requested before the dependent row loads
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (threadIdx.x + 256 * i) * 4;
+    if (c < d) {
+      gg[i] = *reinterpret_cast<const floatx4*>(gamma + c);
+      bb[i] = *reinterpret_cast<const floatx4*>(beta + c);
+    }
+  }
   const int p = pos_dev[r];
   if (lens && threadIdx.x == 0) lens[r] = p + 1;
   const float* a = w_tok + (size_t)tok[r] * d;
@@ -906,11 +924,9 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(const float* __restrict__
   for (int i = 0; i < 4; ++i) {
     const int c = (threadIdx.x + 256 * i) * 4;
     if (c < d) {
-      const floatx4 gg = *reinterpret_cast<const floatx4*>(gamma + c);
-      const floatx4 bb = *reinterpret_cast<const floatx4*>(beta + c);
       floatx4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (xv[i][e] - mu) * is * gg[e] + bb[e];
+      for (int e = 0; e < 4; ++e) o[e] = (xv[i][e] - mu) * is * gg[i][e] + bb[i][e];
       *reinterpret_cast<floatx4*>(y + (size_t)r * d + c) = o;
     }
   }

@@ -180,6 +180,78 @@ def time_region(ctx, fn, steps: int) -> float:
     return ms
 
 
+def bench_ceilings(ctx, cus: int) -> dict:
+    """What this GPU sustains, measured with the probes of
+    aurora_amd/probes/ceilings.hip on the library's stream: fp32 MFMA with
+    register operands (2 blocks of 4 waves per CU, 8 independent chains per
+    wave), a streaming read of 2 GiB (the best of 2-16 blocks per CU with 4
+    or 8 float4 loads in flight per lane), and an empty kernel replayed from a HIP graph (per
+    launch, over 100 captured launches).  The roofline fractions keep the
+    published peaks; these say how much of them the silicon reaches."""
+    import ctypes as C
+
+    from aurora_amd.build import PROBE_LIB
+    from aurora_amd.gpu import GpuBuffer, _lib
+
+    if not PROBE_LIB.exists():
+        raise RuntimeError(f"{PROBE_LIB} is missing: run __graft_entry__.build()")
+    lib = C.CDLL(str(PROBE_LIB))
+    lib.ceil_mfma_f32_flop.restype = C.c_double
+    lib.ceil_mfma_f32_flop.argtypes = [C.c_int, C.c_int]
+    lib.ceil_mfma_f32.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+    lib.ceil_stream_read.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_void_p]
+    lib.ceil_graph_create.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_void_p)]
+    lib.ceil_graph_launch.argtypes = [C.c_void_p, C.c_void_p]
+    lib.ceil_graph_destroy.argtypes = [C.c_void_p]
+    stream = _lib.load().aur_stream(ctx.ptr)
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with HIP error {rc}")
+
+    mfma_blocks, iters = 2 * cus, 20000
+    sink = GpuBuffer.empty(ctx, 16 * cus * 256)
+    ramp_end = time.perf_counter() + CLOCK_RAMP_S
+    while time.perf_counter() < ramp_end:
+        ok(lib.ceil_mfma_f32(stream, mfma_blocks, iters, sink.ptr), "ceil_mfma_f32")
+        ctx.sync()
+    ms = time_region(ctx, lambda: ok(lib.ceil_mfma_f32(stream, mfma_blocks, iters, sink.ptr), "ceil_mfma_f32"), 5)
+    mfma_tf = lib.ceil_mfma_f32_flop(mfma_blocks, iters) / (ms * 1e-3) / 1e12
+
+    nbytes = 2 << 30
+    src = GpuBuffer.zeros(ctx, nbytes // 4)
+    reads = {}
+    for mode, depth in ((0, "4 loads"), (1, "8 loads"), (2, "8 non-temporal loads")):
+        for per_cu in (2, 4, 8, 16):
+            blocks = per_cu * cus
+
+            def rd(mode=mode, blocks=blocks):
+                ok(lib.ceil_stream_read(stream, src.ptr, nbytes, blocks, mode, sink.ptr), "ceil_stream_read")
+
+            for _ in range(2):
+                rd()
+            reads[f"{depth}, {per_cu} blocks/CU"] = nbytes / (time_region(ctx, rd, 5) * 1e-3) / 1e9
+    best = max(reads, key=reads.get)
+    read_gbs = reads[best]
+    src.free()
+
+    n_launch = 100
+    ex = C.c_void_p()
+    ok(lib.ceil_graph_create(stream, n_launch, C.byref(ex)), "ceil_graph_create")
+    for _ in range(5):
+        ok(lib.ceil_graph_launch(stream, ex), "ceil_graph_launch")
+    ms_g = time_region(ctx, lambda: ok(lib.ceil_graph_launch(stream, ex), "ceil_graph_launch"), 20)
+    ok(lib.ceil_graph_destroy(ex), "ceil_graph_destroy")
+    sink.free()
+    out = {"mfma_fp32_tflops": round(mfma_tf, 1), "mfma_fp32_frac_of_peak": round(mfma_tf / PEAK_FP32_MFMA, 3),
+           "hbm_read_gbs": round(read_gbs, 1), "hbm_read_frac_of_peak": round(read_gbs / PEAK_HBM, 3),
+           "hbm_read_best": best, "hbm_read_all_gbs": {k: round(v, 1) for k, v in reads.items()},
+           "graph_empty_kernel_us": round(ms_g * 1e3 / n_launch, 2),
+           "probes": "register-operand fp32 MFMA (16x16x4), 2 GiB streaming read, empty kernel in a HIP graph"}
+    log(f"[bench] ceilings {out}")
+    return out
+
+
 C3 = dict(vocab=8192, d_model=1024, n_layer=12, n_head=16, d_ff=4096, seq_len_max=1024)
 
 
@@ -492,7 +564,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["head", "sweep", "train", "decode", "attention", "traffic", "shapes"],
+    ap.add_argument("--only", choices=["head", "sweep", "train", "decode", "attention", "traffic", "shapes",
+                                       "ceilings"],
                     default=None,
                     help="profile helper: time only this part and skip the CPU baseline")
     ap.add_argument("--decode-steps", type=int, default=256)
@@ -553,6 +626,9 @@ def main() -> int:
     if args.only == "shapes":
         bench_c3_and_shards(ctx, args.steps)
         return 0
+    if args.only == "ceilings":
+        bench_ceilings(ctx, cus)
+        return 0
 
     def step():
         for _, _, fn in items:
@@ -593,6 +669,7 @@ def main() -> int:
     attn = bench_attention(ctx, max(3, args.steps // 4))
     train = bench_train(ctx, max(2, min(args.steps, 5)), min(args.warmup, 2))
     decode = bench_decode(ctx, args.decode_steps)
+    ceilings = bench_ceilings(ctx, cus)
     host = cpu_host()
     thr = host["threads"]
     cpu = cpu_baseline(thr, args.cpu_budget)
@@ -636,6 +713,7 @@ def main() -> int:
         "attention": attn,
         "train": train,
         "decode": decode,
+        "ceilings": ceilings,
         "roofline": {"bound": "mfma", "kernel": "gemm_f32_mfma_direct<256,128> (tied head, NT 8192x8192x512)",
                      "achieved": round(head_tf, 3), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(head_tf / PEAK_FP32_MFMA, 4), "traffic": round(HEAD_TRAFFIC_BYTES),

@@ -66,3 +66,18 @@ def test_integration_rust_binding_covers_the_header():
     text = (ROOT / "INTEGRATION.md").read_text()
     missing = [n for n in sorted(declared_functions()) if f"pub fn {n}(" not in text]
     assert not missing, missing
+
+
+def test_ceiling_probe_library_loads():
+    """The bench's roofline ceiling probes (a separate library, not the C
+    ABI) are built and export what bench.py binds; the FLOP helper is pure
+    arithmetic: blocks · 4 waves · iters · 4 rounds · 8 chains · 2048."""
+    from aurora_amd.build import PROBE_LIB
+
+    lib = C.CDLL(str(PROBE_LIB))
+    for name in ("ceil_mfma_f32", "ceil_mfma_f32_flop", "ceil_stream_read", "ceil_graph_create",
+                 "ceil_graph_launch", "ceil_graph_destroy"):
+        assert hasattr(lib, name), name
+    lib.ceil_mfma_f32_flop.restype = C.c_double
+    lib.ceil_mfma_f32_flop.argtypes = [C.c_int, C.c_int]
+    assert lib.ceil_mfma_f32_flop(512, 10) == 512 * 4 * 10 * 4 * 8 * 2048
