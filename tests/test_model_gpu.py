@@ -344,6 +344,34 @@ def test_kv_decode_matches_cpu_generate_step(ctx):
     m.destroy()
 
 
+def test_kv_decode_above_64_sequences_matches_cpu(ctx):
+    """More than 64 sequences: the decode step runs eagerly (no captured
+    graph) with the tiled GEMMs and their residual epilogues instead of the
+    decode K-range kernels; every sequence against the oracle."""
+    cfg = OM.Config(vocab=64, d_model=64, n_layer=2, n_head=4, d_ff=128, seq_len_max=32)
+    P = OM.init_params(cfg, 23)
+    B, T0, steps = 72, 10, 3
+    rng = np.random.default_rng(23)
+    prompts = rng.integers(0, cfg.vocab, (B, T0)).astype(np.uint32)
+    feed = rng.integers(0, cfg.vocab, (steps, B)).astype(np.uint32)
+    m = _gpu_model(ctx, cfg, B, P)
+    cache = m.kv_cache(B, cfg.seq_len_max)
+    last = m.prefill_kv(cache, prompts)
+    cpu = [OM.KvCache(cfg) for _ in range(B)]
+    for b in range(B):
+        full = cpu[b].prefill(P, prompts[b])
+        assert fro_rel(last[b], full.reshape(T0, -1)[-1]) < 1e-4, b
+    for s in range(steps):
+        logits, nxt = m.generate_step_kv(cache, feed[s])
+        for b in range(B):
+            want = OM.generate_step(P, cfg, cpu[b], int(feed[s, b]))
+            assert fro_rel(logits[b], want) < 1e-4, (s, b)
+        assert np.array_equal(nxt, logits.argmax(1)), s
+    assert cache.current_len == T0 + steps
+    cache.destroy()
+    m.destroy()
+
+
 @pytest.mark.parametrize("d,H,F", [(384, 6, 1536), (768, 12, 3072), (640, 10, 2560), (384, 8, 1536),
                                    (96, 4, 192)])
 def test_kv_decode_widths_match_cpu(ctx, d, H, F):
