@@ -252,6 +252,43 @@ def bench_ceilings(ctx, cus: int) -> dict:
     return out
 
 
+def bench_vendor(steps: int) -> None:
+    """The vendor library on this bench's GEMM shapes, for comparison only
+    (not part of the product path): torch.matmul (hipBLASLt) fp32 A@Bᵀ and
+    A@B after the same clock ramp, timed with torch events over `steps`
+    calls.  Runs in a process that never loads libaurora_hip.so: torch ships
+    its own HIP runtime, and the two do not share one process on this image.
+    This library's figures for the same shapes come from --only sweep /
+    --only shapes."""
+    import torch
+
+    shapes = [(8192, 8192, 512), (8192, 1536, 512), (8192, 512, 512), (8192, 512, 2048),
+              (16384, 3072, 1024), (16384, 1024, 4096), (16384, 4096, 1024),
+              (1024, 1536, 512), (1024, 512, 512), (1024, 512, 2048), (2048, 1024, 1024)]
+    dev = torch.device("cuda", 0)
+    log(f"[bench] vendor: torch {torch.__version__} on {torch.cuda.get_device_name(0)}")
+    for m, n, k in shapes:
+        x = torch.rand(m, k, device=dev) - 0.5
+        w = torch.rand(n, k, device=dev) - 0.5
+        wt = w.t().contiguous()
+        res = {}
+        for form, fn in (("NT", lambda: x @ w.t()), ("NN", lambda: x @ wt)):
+            end = time.perf_counter() + CLOCK_RAMP_S
+            while time.perf_counter() < end:
+                for _ in range(10):
+                    fn()
+                torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            res[form] = 2.0 * m * n * k / (e0.elapsed_time(e1) / steps * 1e-3) / 1e12
+        log(f"[bench] vendor {m}x{n}x{k}: NT {res['NT']:.1f} NN {res['NN']:.1f} TFLOP/s")
+        del x, w, wt
+
+
 C3 = dict(vocab=8192, d_model=1024, n_layer=12, n_head=16, d_ff=4096, seq_len_max=1024)
 
 
@@ -565,7 +602,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", choices=["head", "sweep", "train", "decode", "attention", "traffic", "shapes",
-                                       "ceilings"],
+                                       "ceilings", "vendor"],
                     default=None,
                     help="profile helper: time only this part and skip the CPU baseline")
     ap.add_argument("--decode-steps", type=int, default=256)
@@ -579,6 +616,10 @@ def main() -> int:
         print("bench.py: this build measures ONE GPU only (every box has one GPU; "
               "sharding across GPUs is designed, not built)", file=sys.stderr)
         return 2
+
+    if args.only == "vendor":  # before anything loads libaurora_hip.so
+        bench_vendor(args.steps)
+        return 0
 
     from aurora_amd.gpu import GpuContext
 
