@@ -1275,6 +1275,14 @@ int aur_gemm_ex(aur_ctx* ctx, int a_kcontig, int b_kcontig, const float* a, uint
                 const float* b, uint32_t ldb, float* c, uint32_t ldc, uint32_t m, uint32_t n,
                 uint32_t k, int accumulate) {
   AUR_CHECK_CTX(ctx);
+  // A row of each operand must fit its leading dimension (otherwise the last
+  // rows read and write past the buffers), and every extent must fit an int.
+  constexpr uint32_t kMax = 0x7fffffffu;
+  if (m > kMax || n > kMax || k > kMax || lda > kMax || ldb > kMax || ldc > kMax)
+    return aur::set_error(ctx, AUR_ELIMIT, "gemm_ex: extents above 2^31 - 1");
+  if (lda < (a_kcontig ? k : m) || ldb < (b_kcontig ? k : n) || ldc < n)
+    return aur::set_error(ctx, AUR_EINVAL, "gemm_ex: leading dimension below the row length (lda=%u ldb=%u ldc=%u)",
+                          lda, ldb, ldc);
   return aur::gemm(ctx, a_kcontig != 0, b_kcontig != 0, a, (int)lda, b, (int)ldb, c, (int)ldc,
                    (int)m, (int)n, (int)k, accumulate != 0);
 }

@@ -116,7 +116,9 @@ int aur_outer_accum_noalloc(aur_ctx* ctx, const float* x, const float* d_y, floa
  * explicit leading dimensions).
  *   a_kcontig != 0 : A(m,k) = a[m*lda + k]   else A(m,k) = a[k*lda + m]
  *   b_kcontig != 0 : B(k,n) = b[n*ldb + k]   else B(k,n) = b[k*ldb + n]
- *   C(m,n) = c[m*ldc + n];  accumulate != 0 → C += A·B  else C = A·B. */
+ *   C(m,n) = c[m*ldc + n];  accumulate != 0 → C += A·B  else C = A·B.
+ * AUR_EINVAL when lda < (a_kcontig ? k : m), ldb < (b_kcontig ? k : n) or
+ * ldc < n; AUR_ELIMIT for an extent above 2^31 - 1. */
 int aur_gemm_ex(aur_ctx* ctx, int a_kcontig, int b_kcontig,
                 const float* a, uint32_t lda, const float* b, uint32_t ldb,
                 float* c, uint32_t ldc, uint32_t m, uint32_t n, uint32_t k,

@@ -332,3 +332,32 @@ def test_split_k_refused_while_captured(ctx, monkeypatch):
         x.free()
     cw, fr = _gates(got, a.reshape(m, k).astype(np.float64), b.reshape(n, k).T.astype(np.float64))
     assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
+
+
+def test_gemm_ex_rejects_short_leading_dimensions(ctx):
+    """aur_gemm_ex refuses a leading dimension shorter than the operand's row
+    (lda < k for a k-contiguous A, < m for a k-strided one; likewise ldb with
+    k / n; ldc < n) and extents above 2^31 - 1, before anything is launched;
+    the same call with the minimal leading dimensions runs."""
+    from aurora_amd._lib import AuroraError
+    from aurora_amd.gpu import GpuBuffer
+
+    m, n, k = 64, 48, 32
+    rng = np.random.default_rng(33)
+    a, b = _u(rng, m * k), _u(rng, n * k)
+    ab, bb, cb = GpuBuffer.from_slice(ctx, a), GpuBuffer.from_slice(ctx, b), GpuBuffer.zeros(ctx, m * n)
+    bad = [(1, 1, k - 4, k, n), (0, 1, m - 4, k, n), (1, 1, k, k - 4, n), (1, 0, k, n - 4, n),
+           (1, 1, k, k, n - 4)]
+    for ak, bk, lda, ldb, ldc in bad:
+        with pytest.raises(AuroraError) as e:
+            ctx.call("aur_gemm_ex", ak, bk, ab.ptr, lda, bb.ptr, ldb, cb.ptr, ldc, m, n, k, 0)
+        assert e.value.code == 10001 and "leading dimension" in str(e.value), (ak, bk, lda, ldb, ldc)
+    with pytest.raises(AuroraError) as e:
+        ctx.call("aur_gemm_ex", 1, 1, ab.ptr, 1 << 31, bb.ptr, k, cb.ptr, n, m, n, k, 0)
+    assert e.value.code == 10003
+    ctx.call("aur_gemm_ex", 1, 1, ab.ptr, k, bb.ptr, k, cb.ptr, n, m, n, k, 0)
+    got = cb.download()
+    for x in (ab, bb, cb):
+        x.free()
+    cw, fr = _gates(got, a.reshape(m, k).astype(np.float64), b.reshape(n, k).T.astype(np.float64))
+    assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
