@@ -292,6 +292,8 @@ class DecoderTransformerGpu {
   void encode_backward(uint32_t b, uint32_t t);
   void upload_tokens(const uint32_t* tokens, const uint32_t* targets, uint32_t b, uint32_t t);
   void check_cache(const KvCacheGpu& cache) const;
+  void init();              // the constructor's work
+  void release() noexcept;  // frees whatever init() or later calls allocated
 
   aur_ctx* ctx_;
   TransformerConfig cfg_;

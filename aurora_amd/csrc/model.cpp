@@ -105,6 +105,20 @@ struct DecoderTransformerGpu::Acts {
 DecoderTransformerGpu::DecoderTransformerGpu(aur_ctx* ctx, const TransformerConfig& cfg,
                                              uint32_t max_batch)
     : ctx_(ctx), cfg_(cfg), max_batch_(max_batch) {
+  // A constructor that throws runs no destructor: free what was allocated
+  // before the failure (an activation arena too large for the device, say).
+  try {
+    init();
+  } catch (...) {
+    release();
+    throw;
+  }
+}
+
+void DecoderTransformerGpu::init() {
+  const TransformerConfig& cfg = cfg_;
+  aur_ctx* ctx = ctx_;
+  const uint32_t max_batch = max_batch_;
   const size_t V = cfg.vocab, d = cfg.d_model, L = cfg.n_layer, F = cfg.d_ff, Tm = cfg.seq_len_max;
   if (!ctx || V == 0 || d == 0 || L == 0 || F == 0 || Tm == 0 || max_batch == 0 || cfg.n_head == 0 ||
       d % cfg.n_head != 0)
@@ -246,16 +260,23 @@ DecoderTransformerGpu::~DecoderTransformerGpu() {
     c->drop_graph();
     c->owner_ = nullptr;
   }
+  release();
+}
+
+void DecoderTransformerGpu::release() noexcept {
   if (ctx_) {
     aur_sync(ctx_);
     if (acts_ && acts_->pin) (void)hipHostFree(acts_->pin);
     if (acts_ && acts_->pin_done) (void)hipEventDestroy(acts_->pin_done);
-    aur_free(ctx_, act_mem_);
-    aur_free(ctx_, state_mem_);
+    if (act_mem_) aur_free(ctx_, act_mem_);
+    if (state_mem_) aur_free(ctx_, state_mem_);
     if (muon_mem_) aur_free(ctx_, muon_mem_);
   }
+  act_mem_ = state_mem_ = muon_mem_ = nullptr;
   delete layers_;
   delete acts_;
+  layers_ = nullptr;
+  acts_ = nullptr;
 }
 
 float* DecoderTransformerGpu::tensor(const std::string& name, int layer, bool grad, size_t* n) const {
@@ -724,11 +745,14 @@ KvCacheGpu::KvCacheGpu(DecoderTransformerGpu& model, uint32_t batch_, uint32_t m
   pos_ = cv.take<int32_t>(B);
   lens_ = cv.take<int32_t>(B);
   tok_ = cv.take<uint32_t>(B);
-  if (cv.off > bytes_) {
+  try {
+    if (cv.off > bytes_) throw Error("KvCacheGpu: arena overflow", AUR_ENOMEM);
+    reset();
+  } catch (...) {  // no destructor runs for a constructor that throws
     aur_free(ctx_, mem_);
-    throw Error("KvCacheGpu: arena overflow", AUR_ENOMEM);
+    mem_ = nullptr;
+    throw;
   }
-  reset();
   model.caches_.push_back(this);
 }
 

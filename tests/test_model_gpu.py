@@ -437,3 +437,35 @@ def test_greedy_kv_decode_token_identical_to_full_forward(ctx):
     assert cpu_seq == list(kv_seq[0, T0:]), (cpu_seq, kv_seq[0, T0:])
     cache.destroy()
     m.destroy()
+
+
+def test_failed_model_create_frees_its_memory(ctx):
+    """A model whose activation arena cannot be allocated (max_batch 4096 at
+    the config-3 width asks for about a terabyte) fails with the allocator's
+    hipErrorOutOfMemory (2), and
+    what its constructor had already allocated (parameters, gradients and
+    moments, 0.5 GB here) is freed: the device's free memory is back where
+    it was, and a model of the same width with a small batch still builds."""
+    import ctypes
+
+    from aurora_amd._lib import AuroraError
+    from aurora_amd.model import DecoderTransformerGpu
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemGetInfo.argtypes = [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]
+
+    def free_bytes():
+        ctx.sync()
+        f, t = ctypes.c_size_t(), ctypes.c_size_t()
+        assert hip.hipMemGetInfo(ctypes.byref(f), ctypes.byref(t)) == 0
+        return f.value
+
+    before = free_bytes()
+    for _ in range(3):
+        with pytest.raises(AuroraError) as e:
+            DecoderTransformerGpu(ctx, 8192, 1024, 2, 16, 4096, 1024, 4096)
+        assert e.value.code == 2, e.value  # hipErrorOutOfMemory from hipMalloc
+    after = free_bytes()
+    assert before - after < (64 << 20), (before, after)
+    m = DecoderTransformerGpu(ctx, 8192, 1024, 2, 16, 4096, 1024, 1)
+    m.destroy()
