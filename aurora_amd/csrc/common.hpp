@@ -31,6 +31,11 @@ namespace aur {
 
 int set_error(aur_ctx* ctx, int code, const char* fmt, ...);
 
+inline void bind_device(const aur_ctx* ctx) {
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur != ctx->device) (void)hipSetDevice(ctx->device);
+}
+
 // Makes `ctx` own at least `bytes` of workspace; returns 0 or an error code.
 int ensure_workspace(aur_ctx* ctx, size_t bytes);
 
@@ -84,9 +89,13 @@ int gemm_nt_partials(aur_ctx* ctx, const float* A, int lda, const float* B, int 
 
 }  // namespace aur
 
+// Every entry point: a null context is refused, and the context's device is
+// made current for the calling thread, so allocations and launches of one
+// context go to its own GPU when a process drives several.
 #define AUR_CHECK_CTX(ctx)                                   \
   do {                                                       \
     if ((ctx) == nullptr) return AUR_EINVAL;                 \
+    aur::bind_device(ctx);                                   \
   } while (0)
 
 // Records a failing HIP call in the context and returns its code.

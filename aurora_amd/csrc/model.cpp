@@ -959,6 +959,7 @@ struct aur_kv_cache {
 namespace {
 template <class F>
 int guard(aur_ctx* ctx, F&& f) {
+  if (ctx) aur::bind_device(ctx);  // the model's GPU, whichever device the thread had current
   try {
     f();
     return 0;

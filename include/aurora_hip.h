@@ -43,7 +43,10 @@ typedef struct aur_ctx aur_ctx;
 
 /* Create a context on HIP device `device` with one default-priority stream.
  * Mirrors GpuContext::new() -> Result<Self, GpuInitError> (context.rs:22):
- * the only fallible constructor; non-zero when no usable gfx950 device. */
+ * the only fallible constructor; non-zero when no usable gfx950 device.
+ * Every call taking a context (or a model / cache made from one) first makes
+ * that context's device current for the calling thread, so a process may
+ * drive one context per GPU from one thread. */
 int aur_init(int device, aur_ctx** out);
 int aur_destroy(aur_ctx* ctx);
 /* Message of the last failing call on this context ("" if none). ctx may be
