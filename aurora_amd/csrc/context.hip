@@ -14,6 +14,11 @@ std::string g_init_err;
 namespace aur {
 
 int set_error(aur_ctx* ctx, int code, const char* fmt, ...) {
+  // A failing HIP call also stays behind as the runtime's sticky "last
+  // error", which the next launch check (hipGetLastError) would report
+  // against an unrelated kernel — a failed hipMalloc would fail the next
+  // launch.  Every failure this library reports passes here: consume it.
+  (void)hipGetLastError();
   char buf[512];
   va_list ap;
   va_start(ap, fmt);
