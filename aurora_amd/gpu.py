@@ -137,7 +137,9 @@ class GpuBuffer:
         self.ctx.call("aur_h2d", self.ptr, arr.ctypes.data, arr.nbytes)
 
     def download(self, n: int | None = None) -> np.ndarray:
-        n = self.len if n is None else n
+        n = self.len if n is None else int(n)
+        if not 0 <= n <= self.len:
+            raise ValueError(f"download of {n} elements from buffer of {self.len}")
         out = np.empty(n, dtype=self.dtype)
         self.ctx.call("aur_d2h", out.ctypes.data, self.ptr, out.nbytes)
         return out
