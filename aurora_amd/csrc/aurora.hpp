@@ -96,9 +96,23 @@ class GpuBuffer {
   size_t len_;
 };
 
+// The kernels read and write exactly the extents their dimensions name; a
+// buffer shorter than that is refused here, where its length is known (the
+// reference's WGSL had wgpu's bounds-checked buffer access instead — an
+// out-of-range access on the GPU faults).
+inline void need(const GpuBuffer<float>& b, size_t n, const char* what) {
+  if (b.len() < n)
+    throw Error(std::string(what) + ": buffer of " + std::to_string(b.len()) + " floats, " +
+                    std::to_string(n) + " needed",
+                AUR_EINVAL);
+}
+
 struct GemmKernel {
   void dispatch_into(const GpuContext& c, const GpuBuffer<float>& a, const GpuBuffer<float>& b,
                      const GpuBuffer<float>& out, uint32_t m, uint32_t n, uint32_t k) const {
+    need(a, (size_t)m * k, "GemmKernel a");
+    need(b, (size_t)k * n, "GemmKernel b");
+    need(out, (size_t)m * n, "GemmKernel c");
     check(c.raw(), aur_gemm_nn(c.raw(), a.ptr(), b.ptr(), out.ptr(), m, n, k), "GemmKernel");
   }
 };
@@ -106,6 +120,9 @@ struct GemmKernel {
 struct GemmTransposeBKernel {
   void dispatch_into(const GpuContext& c, const GpuBuffer<float>& a, const GpuBuffer<float>& b,
                      const GpuBuffer<float>& out, uint32_t m, uint32_t n, uint32_t k) const {
+    need(a, (size_t)m * k, "GemmTransposeBKernel a");
+    need(b, (size_t)n * k, "GemmTransposeBKernel b");
+    need(out, (size_t)m * n, "GemmTransposeBKernel c");
     check(c.raw(), aur_gemm_nt(c.raw(), a.ptr(), b.ptr(), out.ptr(), m, n, k), "GemmTransposeBKernel");
   }
 };
@@ -113,6 +130,9 @@ struct GemmTransposeBKernel {
 struct OuterProductAccumKernel {
   void dispatch_into(const GpuContext& c, const GpuBuffer<float>& x, const GpuBuffer<float>& d_y,
                      const GpuBuffer<float>& dest, uint32_t d_out, uint32_t d_in, uint32_t t) const {
+    need(x, (size_t)t * d_in, "OuterProductAccumKernel x");
+    need(d_y, (size_t)t * d_out, "OuterProductAccumKernel d_y");
+    need(dest, (size_t)d_out * d_in, "OuterProductAccumKernel dest");
     check(c.raw(), aur_outer_accum(c.raw(), x.ptr(), d_y.ptr(), dest.ptr(), d_out, d_in, t),
           "OuterProductAccumKernel");
   }
@@ -123,6 +143,9 @@ struct CausalMhaForwardKernel {
   void dispatch_into(const GpuContext& c, const GpuBuffer<float>& q, const GpuBuffer<float>& k,
                      const GpuBuffer<float>& v, const GpuBuffer<float>& out, const GpuBuffer<float>& lse,
                      uint32_t t, uint32_t n_head, uint32_t d_head, uint32_t b = 1) const {
+    const size_t act = (size_t)b * t * n_head * d_head;
+    for (const GpuBuffer<float>* x : {&q, &k, &v, &out}) need(*x, act, "CausalMhaForwardKernel q/k/v/out");
+    need(lse, (size_t)b * n_head * t, "CausalMhaForwardKernel lse");
     check(c.raw(), aur_mha_fwd(c.raw(), q.ptr(), k.ptr(), v.ptr(), out.ptr(), lse.ptr(), b, t, n_head, d_head),
           "CausalMhaForwardKernel");
   }
@@ -138,6 +161,11 @@ struct CausalMhaBackwardKernel {
                      const GpuBuffer<float>& d_out, const GpuBuffer<float>& dq, const GpuBuffer<float>& dk,
                      const GpuBuffer<float>& dv, const GpuBuffer<float>& ws, uint32_t t, uint32_t n_head,
                      uint32_t d_head, uint32_t b = 1) const {
+    const size_t act = (size_t)b * t * n_head * d_head;
+    for (const GpuBuffer<float>* x : {&q, &k, &v, &out, &d_out, &dq, &dk, &dv})
+      need(*x, act, "CausalMhaBackwardKernel q/k/v/out/d_out/dq/dk/dv");
+    need(lse, (size_t)b * n_head * t, "CausalMhaBackwardKernel lse");
+    need(ws, workspace_len(t, n_head, b), "CausalMhaBackwardKernel workspace");
     check(c.raw(),
           aur_mha_bwd(c.raw(), q.ptr(), k.ptr(), v.ptr(), out.ptr(), lse.ptr(), d_out.ptr(), dq.ptr(),
                       dk.ptr(), dv.ptr(), ws.ptr(), b, t, n_head, d_head),
@@ -153,6 +181,12 @@ struct MhaKvCacheKernel {
                      const GpuBuffer<float>& v_history, const GpuBuffer<float>& out,
                      const GpuBuffer<float>& scratch, uint32_t t_total, uint32_t n_head, uint32_t d_head,
                      uint32_t max_len) const {
+    const size_t d = (size_t)n_head * d_head;
+    need(q_new, d, "MhaKvCacheKernel q_new");
+    need(out, d, "MhaKvCacheKernel out");
+    need(k_history, (size_t)max_len * d, "MhaKvCacheKernel k_history");
+    need(v_history, (size_t)max_len * d, "MhaKvCacheKernel v_history");
+    need(scratch, scratch_len(n_head, max_len), "MhaKvCacheKernel scratch");
     check(c.raw(),
           aur_mha_kv_step(c.raw(), q_new.ptr(), k_history.ptr(), v_history.ptr(), out.ptr(), scratch.ptr(),
                           t_total, n_head, d_head, max_len),

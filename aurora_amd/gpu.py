@@ -157,6 +157,16 @@ def _p(buf) -> int:
     return buf.ptr if isinstance(buf, GpuBuffer) else int(buf)
 
 
+def _need(what: str, n: int, *bufs) -> None:
+    """The kernels touch exactly the extents their dimensions name; a
+    GpuBuffer shorter than that is refused before the launch (the reference's
+    WGSL had wgpu's bounds-checked buffer access; an out-of-range access on the
+    GPU faults).  Raw device pointers carry no length and pass unchecked."""
+    for b in bufs:
+        if isinstance(b, GpuBuffer) and b.len < n:
+            raise ValueError(f"{what}: buffer of {b.len} elements, {n} needed")
+
+
 class _Kernel:
     @classmethod
     def new(cls, ctx: GpuContext | None = None):
@@ -167,6 +177,9 @@ class GemmKernel(_Kernel):
     """C = A·B (src/gpu/matmul.rs:230-356)."""
 
     def dispatch_into(self, ctx, a, b, c, m, n, k):
+        _need("GemmKernel a", m * k, a)
+        _need("GemmKernel b", k * n, b)
+        _need("GemmKernel c", m * n, c)
         ctx.call("aur_gemm_nn", _p(a), _p(b), _p(c), m, n, k)
 
 
@@ -174,6 +187,9 @@ class GemmTransposeBKernel(_Kernel):
     """C = A·Bᵀ (src/gpu/matmul.rs:358-409)."""
 
     def dispatch_into(self, ctx, a, b, c, m, n, k):
+        _need("GemmTransposeBKernel a", m * k, a)
+        _need("GemmTransposeBKernel b", n * k, b)
+        _need("GemmTransposeBKernel c", m * n, c)
         ctx.call("aur_gemm_nt", _p(a), _p(b), _p(c), m, n, k)
 
 
@@ -181,6 +197,9 @@ class OuterProductAccumKernel(_Kernel):
     """dest[d_out,d_in] += Σ_t d_y[t,d_out]·x[t,d_in] (src/gpu/reduce.rs:125-241)."""
 
     def dispatch_into(self, ctx, x, d_y, dest, d_out, d_in, t):
+        _need("OuterProductAccumKernel x", t * d_in, x)
+        _need("OuterProductAccumKernel d_y", t * d_out, d_y)
+        _need("OuterProductAccumKernel dest", d_out * d_in, dest)
         ctx.call("aur_outer_accum", _p(x), _p(d_y), _p(dest), d_out, d_in, t)
 
 
@@ -191,6 +210,8 @@ class CausalMhaForwardKernel(_Kernel):
     """
 
     def dispatch_into(self, ctx, q, k, v, out, lse, t, n_head, d_head, b=1):
+        _need("CausalMhaForwardKernel q/k/v/out", b * t * n_head * d_head, q, k, v, out)
+        _need("CausalMhaForwardKernel lse", b * n_head * t, lse)
         ctx.call("aur_mha_fwd", _p(q), _p(k), _p(v), _p(out), _p(lse), b, t, n_head, d_head)
 
 
@@ -203,6 +224,9 @@ class CausalMhaBackwardKernel(_Kernel):
 
     def dispatch_into(self, ctx, q, k, v, out, lse, d_out, dq, dk, dv, ws, t, n_head,
                       d_head, b=1):
+        _need("CausalMhaBackwardKernel tensors", b * t * n_head * d_head, q, k, v, out, d_out, dq, dk, dv)
+        _need("CausalMhaBackwardKernel lse", b * n_head * t, lse)
+        _need("CausalMhaBackwardKernel workspace", self.workspace_len(t, n_head, b), ws)
         ctx.call("aur_mha_bwd", _p(q), _p(k), _p(v), _p(out), _p(lse), _p(d_out), _p(dq),
                  _p(dk), _p(dv), _p(ws), b, t, n_head, d_head)
 
@@ -216,10 +240,16 @@ class MhaKvCacheKernel(_Kernel):
 
     def dispatch_into(self, ctx, q_new, k_history, v_history, out, scratch, t_total, n_head,
                       d_head, max_len):
+        _need("MhaKvCacheKernel q_new/out", n_head * d_head, q_new, out)
+        _need("MhaKvCacheKernel history", max_len * n_head * d_head, k_history, v_history)
+        _need("MhaKvCacheKernel scratch", self.scratch_len(n_head, max_len), scratch)
         ctx.call("aur_mha_kv_step", _p(q_new), _p(k_history), _p(v_history), _p(out),
                  _p(scratch), t_total, n_head, d_head, max_len)
 
     def dispatch_batched(self, ctx, q_new, k_history, v_history, out, scratch, t_total_dev,
                          t_max, b, n_head, d_head, max_len):
+        _need("MhaKvCacheKernel q_new/out", b * n_head * d_head, q_new, out)
+        _need("MhaKvCacheKernel history", b * max_len * n_head * d_head, k_history, v_history)
+        _need("MhaKvCacheKernel scratch", self.scratch_len(n_head, max_len, b), scratch)
         ctx.call("aur_mha_kv_step_batched", _p(q_new), _p(k_history), _p(v_history),
                  _p(out), _p(scratch), _p(t_total_dev), t_max, b, n_head, d_head, max_len)

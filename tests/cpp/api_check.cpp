@@ -68,6 +68,17 @@ int gpu_checks() {
       acc[o * k + i] = s;
     }
   if (double e = rel(bdest.download(), acc); !(e < 1e-5)) return fail("OuterProductAccumKernel", e);
+  // A buffer shorter than the dimensions name is refused before any launch.
+  {
+    auto short_c = GpuBuffer<float>::zeros(ctx, m * n - 1);
+    bool refused = false;
+    try {
+      aurora::GemmTransposeBKernel{}.dispatch_into(ctx, bx, bw, short_c, m, n, k);
+    } catch (const aurora::Error& e) {
+      refused = e.code == AUR_EINVAL;
+    }
+    if (!refused) return fail("short output buffer accepted", 0);
+  }
 
   // causal attention, t = 24, 2 heads of 16: O against the textbook definition
   const uint32_t t = 24, H = 2, dh = 16, d = H * dh;

@@ -4,6 +4,8 @@ import ctypes as C
 import re
 from pathlib import Path
 
+import pytest
+
 ROOT = Path(__file__).resolve().parents[1]
 
 
@@ -81,3 +83,32 @@ def test_ceiling_probe_library_loads():
     lib.ceil_mfma_f32_flop.restype = C.c_double
     lib.ceil_mfma_f32_flop.argtypes = [C.c_int, C.c_int]
     assert lib.ceil_mfma_f32_flop(512, 10) == 512 * 4 * 10 * 4 * 8 * 2048
+
+
+def test_kernel_structs_refuse_short_buffers():
+    """The Python kernel structs check every GpuBuffer against the extent its
+    dimensions name before anything reaches the library (no GPU needed: the
+    refusal comes first); buffers of exactly the needed length pass the check
+    and reach the (here absent) context."""
+    from aurora_amd.gpu import (CausalMhaForwardKernel, GemmKernel, GemmTransposeBKernel,
+                                GpuBuffer, OuterProductAccumKernel)
+
+    def buf(n):
+        return GpuBuffer(None, 0x1000, n)
+
+    m, n, k = 8, 6, 4
+    cases = [
+        (GemmKernel().dispatch_into, (buf(m * k - 1), buf(k * n), buf(m * n), m, n, k), "GemmKernel a"),
+        (GemmKernel().dispatch_into, (buf(m * k), buf(k * n), buf(m * n - 1), m, n, k), "GemmKernel c"),
+        (GemmTransposeBKernel().dispatch_into, (buf(m * k), buf(n * k - 1), buf(m * n), m, n, k),
+         "GemmTransposeBKernel b"),
+        (OuterProductAccumKernel().dispatch_into, (buf(k * n), buf(k * m), buf(m * n - 1), m, n, k),
+         "OuterProductAccumKernel dest"),
+        (CausalMhaForwardKernel().dispatch_into,
+         (buf(64), buf(64), buf(64), buf(64), buf(2 * 4 - 1), 4, 2, 8), "CausalMhaForwardKernel lse"),
+    ]
+    for fn, args, what in cases:
+        with pytest.raises(ValueError, match=what):
+            fn(None, *args)
+    with pytest.raises(AttributeError):  # the check passed; the absent context is reached
+        GemmKernel().dispatch_into(None, buf(m * k), buf(k * n), buf(m * n), m, n, k)
