@@ -287,6 +287,44 @@ def test_config1_weight_grad_accumulate(ctx):
     assert np.array_equal(got, again)
 
 
+def test_tied_lm_head_gradient_through_both_paths(ctx):
+    """tests/gpu_parity.rs:404-467 (tied_lm_head_gradient_matches_cpu_through_both_paths):
+    t = 6, d = 16, V = 24.  Logits = h·w_tokᵀ through GemmTransposeBKernel, the
+    gradient into h = upstream·w_tok through GemmKernel, both against the CPU
+    restatement (tied_lm_head_forward / lm_head_backward, src/transformer/
+    embedding.rs:152-206) at the reference's pointwise 5e-2; here also the
+    w_tok gradient (upstreamᵀ·h, which the reference test leaves to the CPU)
+    through OuterProductAccumKernel into a non-zero gradient, and all three
+    against float64 at the GEMM gates."""
+    from aurora_amd.gpu import GemmKernel, GemmTransposeBKernel, GpuBuffer, OuterProductAccumKernel
+
+    t, d, v = 6, 16, 24
+    rng = np.random.default_rng(0xACE)
+    w_tok = (rng.standard_normal(v * d) * 0.02).astype(np.float32)
+    h, up = _u(rng, t * d), _u(rng, t * v)
+    dw0 = _u(rng, v * d)
+    want_logits = oracle.tied_head_forward(h, w_tok, v, d)
+    want_dw = dw0.copy()
+    want_dh = oracle.lm_head_backward(h, w_tok, up, want_dw, v, d)
+    hb, wb, ub = (GpuBuffer.from_slice(ctx, x) for x in (h, w_tok, up))
+    logits, dh, dw = GpuBuffer.zeros(ctx, t * v), GpuBuffer.zeros(ctx, t * d), GpuBuffer.from_slice(ctx, dw0)
+    GemmTransposeBKernel.new(ctx).dispatch_into(ctx, hb, wb, logits, t, v, d)
+    GemmKernel.new(ctx).dispatch_into(ctx, ub, wb, dh, t, d, v)
+    OuterProductAccumKernel.new(ctx).dispatch_into(ctx, hb, ub, dw, v, d, t)
+    got_logits, got_dh, got_dw = logits.download(), dh.download(), dw.download()
+    for x in (hb, wb, ub, logits, dh, dw):
+        x.free()
+    assert max_rel_err(got_logits, want_logits) < 5e-2
+    assert max_rel_err(got_dh, want_dh) < 5e-2
+    assert max_rel_err(got_dw, want_dw) < 5e-2
+    h64, w64, u64 = (x.astype(np.float64) for x in (h, w_tok, up))
+    for got, a64, b64, c0 in ((got_logits, h64.reshape(t, d), w64.reshape(v, d).T, None),
+                              (got_dh, u64.reshape(t, v), w64.reshape(v, d), None),
+                              (got_dw, u64.reshape(t, v).T, h64.reshape(t, d), dw0.reshape(v, d))):
+        cw, fr = _gates(got, a64, b64, c0)
+        assert cw < TOL_GEMM and fr < TOL_GEMM, (cw, fr)
+
+
 def test_nt_equals_nn_on_materialised_transpose(ctx):
     m, k, n = 300, 257, 190
     rng = np.random.default_rng(7)
