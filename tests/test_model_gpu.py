@@ -469,3 +469,76 @@ def test_failed_model_create_frees_its_memory(ctx):
     assert before - after < (64 << 20), (before, after)
     m = DecoderTransformerGpu(ctx, 8192, 1024, 2, 16, 4096, 1024, 1)
     m.destroy()
+
+
+def _overfit_model(ctx, seed):
+    cfg = OM.Config(vocab=16, d_model=32, n_layer=2, n_head=2, d_ff=64, seq_len_max=16)
+    m = _gpu_model(ctx, cfg, 1, OM.init_params(cfg, seed))
+    tokens = (np.arange(8) % cfg.vocab).astype(np.uint32)
+    return m, tokens, (tokens + 1) % cfg.vocab
+
+
+def test_muon_hybrid_and_adamw_drop_loss_on_overfit(ctx):
+    """tests/gpu_parity.rs:1288-1346 (gpu_muon_hybrid_drops_loss_on_overfit):
+    V16 d32 L2 H2 d_ff64, one 8-token sequence whose target is the next id;
+    five Muon-hybrid steps (muon lr 0.02, momentum 0.95, Nesterov, NS5;
+    AdamW lr 3e-3 without decay on the rest, subset clip 1.0) lower the loss.
+    The same with plain AdamW (clip 1.0, lr 3e-3): the loss falls well below
+    its start within 30 steps."""
+    m, tok, tgt = _overfit_model(ctx, 0x46056)
+    m.zero_grad()
+    initial = m.train_step(tok, tgt)
+    for _ in range(5):
+        m.zero_grad()
+        m.train_step(tok, tgt)
+        m.clip_grads_adamw_subset(1.0)
+        m.step_muon_hybrid(muon_lr=0.02, momentum=0.95, nesterov=True, muon_wd=0.0, ns_steps=5,
+                           lr=3e-3, weight_decay=0.0)
+    m.zero_grad()
+    final = m.train_step(tok, tgt)
+    m.destroy()
+    assert np.isfinite(final) and final < initial, (initial, final)
+
+    m, tok, tgt = _overfit_model(ctx, 0x46057)
+    m.zero_grad()
+    start = m.train_step(tok, tgt)
+    for _ in range(30):
+        m.zero_grad()
+        m.train_step(tok, tgt)
+        m.clip_step_adamw(1.0, lr=3e-3, weight_decay=0.0)
+    m.zero_grad()
+    end = m.train_step(tok, tgt)
+    m.destroy()
+    assert np.isfinite(end) and end < 0.5 * start, (start, end)
+
+
+def test_kv_cache_starts_zeroed_and_reset_matches_fresh(ctx):
+    """tests/kv_cache.rs:446-465 (a new cache's K/V history is all zeros,
+    current_len 0) and :390-444 (after prefill + steps, reset() zeroes the
+    history and current_len, and prefill + step on the reset cache give the
+    logits a fresh cache gives — here bit for bit)."""
+    cfg = OM.Config(vocab=16, d_model=32, n_layer=2, n_head=2, d_ff=64, seq_len_max=16)
+    m = _gpu_model(ctx, cfg, 1, OM.init_params(cfg, 0x9292))
+    fresh = m.kv_cache(1, 16)
+    assert fresh.current_len == 0
+    for layer in range(cfg.n_layer):
+        k, v = fresh.history(layer)
+        assert not np.any(k) and not np.any(v), layer
+    seed_a, seed_b = np.array([[3, 0, 7, 1]], np.uint32), np.array([[5, 2, 9, 11]], np.uint32)
+    m.prefill_kv(fresh, seed_b)
+    want, _ = m.generate_step_kv(fresh, [8])
+    dirty = m.kv_cache(1, 16)
+    m.prefill_kv(dirty, seed_a)
+    m.generate_step_kv(dirty, [4])
+    m.generate_step_kv(dirty, [6])
+    dirty.reset()
+    assert dirty.current_len == 0
+    for layer in range(cfg.n_layer):
+        k, v = dirty.history(layer)
+        assert not np.any(k) and not np.any(v), layer
+    m.prefill_kv(dirty, seed_b)
+    got, _ = m.generate_step_kv(dirty, [8])
+    np.testing.assert_array_equal(got, want)
+    for c in (fresh, dirty):
+        c.destroy()
+    m.destroy()
