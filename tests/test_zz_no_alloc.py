@@ -56,3 +56,60 @@ def test_outer_accum_noalloc_refuses_oversized_partials(ctx):
     assert np.all(dest.download() == 3.0)  # nothing ran
     for b in (bx, bdy, dest):
         b.free()
+
+
+def test_outer_accum_noalloc_replays_from_a_captured_graph(ctx):
+    """The callers this entry point is for capture it into a HIP graph: it
+    captures (nothing in it allocates, synchronises or clears memory), and
+    every replay — with the program's own eager work, a fresh upload of the
+    destination and a synchronisation between replays — equals the eager
+    aur_outer_accum bit for bit."""
+    import ctypes
+
+    from aurora_amd._lib import load
+    from aurora_amd.gpu import GpuBuffer
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    hip.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+    hip.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t]
+    hip.hipGraphLaunch.argtypes = [vp, vp]
+    hip.hipGraphExecDestroy.argtypes = [vp]
+    hip.hipGraphDestroy.argtypes = [vp]
+    stream = load().aur_stream(ctx.ptr)
+
+    d_out, d_in, t = 512, 384, 8192  # split-K plan: partials in the scratch array
+    rng = np.random.default_rng(23)
+    x = rng.uniform(-1, 1, (t, d_in)).astype(np.float32)
+    dy = rng.uniform(-1, 1, (t, d_out)).astype(np.float32)
+    dest0 = rng.uniform(-1, 1, (d_out, d_in)).astype(np.float32)
+    bx, bdy = GpuBuffer.from_slice(ctx, x), GpuBuffer.from_slice(ctx, dy)
+    ref, got = GpuBuffer.from_slice(ctx, dest0), GpuBuffer.from_slice(ctx, dest0)
+    ctx.call("aur_outer_accum", bx.ptr, bdy.ptr, ref.ptr, d_out, d_in, t)
+    want = ref.download()
+
+    ctx.sync()
+    graph, exe = vp(), vp()
+    assert hip.hipStreamBeginCapture(stream, 1) == 0  # hipStreamCaptureModeThreadLocal
+    try:
+        ctx.call("aur_outer_accum_noalloc", bx.ptr, bdy.ptr, got.ptr, d_out, d_in, t)
+    finally:
+        assert hip.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+    try:
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for replay in range(3):
+            got.upload(dest0)
+            # eager work of the program's own between replays
+            ctx.call("aur_outer_accum", bx.ptr, bdy.ptr, ref.ptr, d_out, d_in, t)
+            ctx.sync()
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            ctx.sync()
+            assert np.array_equal(got.download(), want), replay
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        for b in (bx, bdy, ref, got):
+            b.free()
