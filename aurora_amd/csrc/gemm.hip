@@ -955,12 +955,13 @@ constexpr int kBK = 32;
 // MI355X to every forced configuration (6 tiles × split-K 1…16) of 50
 // shapes — the config-1 and config-3 GEMMs of all three forms at M = 8192 /
 // 16384 and at one GPU's 8-way data-parallel share, M = 1024 / 2048 — timed
-// by aurora_amd/tune_gemm.py: tile efficiency 1.00 / 0.95 / 0.85 / 0.70 /
-// 0.55 (128×128 / 128×64 / 64×64 / 64×32 / 32×32), single-block factor 0.8
-// / 0.7 / 0.7 / 0.7 / 0.7, 3 TB/s for the reduction and 2 µs per launch;
-// on the fitting run the pick was within 2.8 % of the measured best on
-// every shape (0.2 % on average).  The two small tiles serve few-tile shapes (M = 1024 with
-// N = 512: 24 → 38 % of peak).
+// by aurora_amd/tune_gemm.py: tile efficiency 1.00 / 0.95 / 0.90 / 0.70 /
+// 0.55 (128×128 / 128×64 / 64×64 / 64×32 / 32×32), single-block factor 0.95
+// / 0.95 / 0.85 / 0.7 / 0.7 (the software-pipelined main loop keeps one
+// wave per SIMD nearly as busy as two), 3 TB/s for the reduction and 2 µs
+// per launch; on the fitting run the pick was within 1.6 % of the measured
+// best on every shape (0.15 % on average).  The two small tiles serve
+// few-tile shapes (M = 1024 with N = 512: 24 → 38 % of peak).
 //
 // allow_wide admits the 256×128 tile (direct-load kernel only: whole tiles,
 // aligned operands, A k-contiguous — with A k-strided it measured 4 % slower
@@ -975,8 +976,8 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int 
     int bm, bn;
     double eff, single;
   };
-  static constexpr Cand cands[] = {{256, 128, 1.03, 0.75}, {128, 128, 1.00, 0.8}, {128, 64, 0.95, 0.7},
-                                   {64, 64, 0.85, 0.7},    {64, 32, 0.70, 0.7},   {32, 32, 0.55, 0.7}};
+  static constexpr Cand cands[] = {{256, 128, 1.03, 0.75}, {128, 128, 1.00, 0.95}, {128, 64, 0.95, 0.95},
+                                   {64, 64, 0.90, 0.85},   {64, 32, 0.70, 0.7},    {32, 32, 0.55, 0.7}};
   Plan p{128, 128, 1, K};
   double best = 1e30;
   for (const Cand& c : cands) {
