@@ -26,6 +26,7 @@
 #include <mutex>
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 namespace {
@@ -482,9 +483,8 @@ __global__ void __launch_bounds__(kThreads, (BM == 256 ? 2 : 1)) gemm_f32_mfma_d
   // MFMA pipe is not left idle while a burst of them issues — which with one
   // or two waves per SIMD nothing else covers (measured on MI355X, C1 sweep
   // 126.5-126.8 → 128.4-129.1 TFLOP/s, 8192×512×2048 A@Bᵀ 124.9 → 129.4).
-  // Past the last stage the loads re-read it into the released stage and the
-  // reads fetch a stage nobody uses: the loop body has no branch, so the
-  // interleave spans it.
+  // The last two stages are peeled (no loads past the end), so the loop body
+  // has no branch and the interleave spans it.
   //   BK = 32: the halves are the two 16-wide k chunks of the stage.
   //   BK = 16 (the 256×128 tile): the halves are the rows i < TM/2 and
   //   i ≥ TM/2 of A; B's fragments are double-buffered.
@@ -508,9 +508,13 @@ __global__ void __launch_bounds__(kThreads, (BM == 256 ? 2 : 1)) gemm_f32_mfma_d
     for (int i = 0; i < H; ++i) fa[i] = TA::frag(smem, wm * WM + i * 16 + l16, 0, g16);
 #pragma unroll
     for (int j = 0; j < TN; ++j) fb[j] = TB::frag(smem + TA::ELEMS, wn * WN + j * 16 + l16, 0, g16);
-    for (int kt = 0; kt < nk; ++kt) {
-      if constexpr (PRE != 0)
-        if (kt == nk - 1) load_epi_operand(g, pre, m0 + wm * WM, n0 + wn * WN, g16, l16, PRE);
+    // One stage.  MODE 0: loads the stage after next; 1 (the second-to-last
+    // stage): loads nothing; 2 (the last): no barrier or next-stage reads
+    // either, and fetches the epilogue operand instead.
+    auto step = [&](int kt, auto mode) {
+      constexpr int MODE = decltype(mode)::value;
+      constexpr bool LAST = MODE == 2;
+      if constexpr (LAST && PRE != 0) load_epi_operand(g, pre, m0 + wm * WM, n0 + wn * WN, g16, l16, PRE);
       const float* sa = smem + (kt & 1) * ST;
 #pragma unroll
       for (int i = H; i < TM; ++i) fa[i] = TA::frag(sa, wm * WM + i * 16 + l16, 0, g16);
@@ -526,15 +530,17 @@ __global__ void __launch_bounds__(kThreads, (BM == 256 ? 2 : 1)) gemm_f32_mfma_d
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       if constexpr (NMF > R1) __builtin_amdgcn_sched_group_barrier(0x008, NMF - R1, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of the next stage landed
-      __syncthreads();
-      __builtin_amdgcn_sched_barrier(0);
-      {
-        float* na = smem + (kt & 1) * ST;
-        const int k0 = kbeg + min(kt + 2, nk - 1) * BK;
-        TA::issue(g.A, g.lda, m0, k0, na, wave, lane);
-        TB::issue(g.B, g.ldb, n0, k0, na + TA::ELEMS, wave, lane);
+      if constexpr (!LAST) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of the next stage landed
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (MODE == 0) {  // into the stage just released
+          float* na = smem + (kt & 1) * ST;
+          const int k0 = kbeg + (kt + 2) * BK;
+          TA::issue(g.A, g.lda, m0, k0, na, wave, lane);
+          TB::issue(g.B, g.ldb, n0, k0, na + TA::ELEMS, wave, lane);
+        }
         const float* xa = smem + ((kt + 1) & 1) * ST;
 #pragma unroll
         for (int i = 0; i < H; ++i) fa[i] = TA::frag(xa, wm * WM + i * 16 + l16, 0, g16);
@@ -547,20 +553,26 @@ __global__ void __launch_bounds__(kThreads, (BM == 256 ? 2 : 1)) gemm_f32_mfma_d
         for (int i = H; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x4(fa[i][s4], fb[j][s4], acc[i][j]);
+      if constexpr (!LAST) {
+        constexpr int NL = MODE == 0 ? L2 : 0;
 #pragma unroll
-      for (int r = 0; r < L2; ++r) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        for (int r = 0; r < NL; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < R2; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (NMF > NL + R2) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NL - R2, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[j] = fbn[j];
       }
-#pragma unroll
-      for (int r = 0; r < R2; ++r) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      if constexpr (NMF > L2 + R2) __builtin_amdgcn_sched_group_barrier(0x008, NMF - L2 - R2, 0);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = fbn[j];
-    }
+    };
+    for (int kt = 0; kt + 2 < nk; ++kt) step(kt, std::integral_constant<int, 0>{});
+    if (nk > 1) step(nk - 2, std::integral_constant<int, 1>{});
+    if (nk > 0) step(nk - 1, std::integral_constant<int, 2>{});
   } else {
     static_assert(BK == 32, "two 16-wide k chunks per stage");
     constexpr int NRD = TM * (AK ? 1 : 4) + TN * (BKC ? 1 : 4);  // DS reads per chunk
@@ -577,9 +589,10 @@ __global__ void __launch_bounds__(kThreads, (BM == 256 ? 2 : 1)) gemm_f32_mfma_d
     for (int i = 0; i < TM; ++i) f0a[i] = TA::frag(smem, wm * WM + i * 16 + l16, 0, g16);
 #pragma unroll
     for (int j = 0; j < TN; ++j) f0b[j] = TB::frag(smem + TA::ELEMS, wn * WN + j * 16 + l16, 0, g16);
-    for (int kt = 0; kt < nk; ++kt) {
-      if constexpr (PRE != 0)
-        if (kt == nk - 1) load_epi_operand(g, pre, m0 + wm * WM, n0 + wn * WN, g16, l16, PRE);
+    auto step = [&](int kt, auto mode) {  // MODE as in the BK = 16 loop
+      constexpr int MODE = decltype(mode)::value;
+      constexpr bool LAST = MODE == 2;
+      if constexpr (LAST && PRE != 0) load_epi_operand(g, pre, m0 + wm * WM, n0 + wn * WN, g16, l16, PRE);
       const float* sa = smem + (kt & 1) * ST;
       const float* sb = sa + TA::ELEMS;
 #pragma unroll
@@ -598,15 +611,17 @@ __global__ void __launch_bounds__(kThreads, (BM == 256 ? 2 : 1)) gemm_f32_mfma_d
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       if constexpr (NMF > R1) __builtin_amdgcn_sched_group_barrier(0x008, NMF - R1, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of the next stage landed
-      __syncthreads();
-      __builtin_amdgcn_sched_barrier(0);
-      {
-        float* na = smem + (kt & 1) * ST;
-        const int k0 = kbeg + min(kt + 2, nk - 1) * BK;
-        TA::issue(g.A, g.lda, m0, k0, na, wave, lane);
-        TB::issue(g.B, g.ldb, n0, k0, na + TA::ELEMS, wave, lane);
+      if constexpr (!LAST) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of the next stage landed
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (MODE == 0) {  // into the stage just released
+          float* na = smem + (kt & 1) * ST;
+          const int k0 = kbeg + (kt + 2) * BK;
+          TA::issue(g.A, g.lda, m0, k0, na, wave, lane);
+          TB::issue(g.B, g.ldb, n0, k0, na + TA::ELEMS, wave, lane);
+        }
         const float* xa = smem + ((kt + 1) & 1) * ST;
 #pragma unroll
         for (int i = 0; i < TM; ++i) f0a[i] = TA::frag(xa, wm * WM + i * 16 + l16, 0, g16);
@@ -619,20 +634,25 @@ __global__ void __launch_bounds__(kThreads, (BM == 256 ? 2 : 1)) gemm_f32_mfma_d
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x4(f1a[i][s4], f1b[j][s4], acc[i][j]);
+      if constexpr (!LAST) {
+        constexpr int NL = MODE == 0 ? L2 : 0;
 #pragma unroll
-      for (int r = 0; r < L2; ++r) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      }
+        for (int r = 0; r < NL; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
 #pragma unroll
-      for (int r = 0; r < R2; ++r) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int r = 0; r < R2; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (NMF > NL + R2) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NL - R2, 0);
       }
-      if constexpr (NMF > L2 + R2) __builtin_amdgcn_sched_group_barrier(0x008, NMF - L2 - R2, 0);
-    }
+    };
+    for (int kt = 0; kt + 2 < nk; ++kt) step(kt, std::integral_constant<int, 0>{});
+    if (nk > 1) step(nk - 2, std::integral_constant<int, 1>{});
+    if (nk > 0) step(nk - 1, std::integral_constant<int, 2>{});
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last, unused loads
 
   if constexpr (PRE != 0) {
     if (nk == 0) load_epi_operand(g, pre, m0 + wm * WM, n0 + wn * WN, g16, l16, PRE);

@@ -35,7 +35,7 @@ COPY_MIB = 256          # calibration copy of the --only traffic leg
 # HBM bytes per head-GEMM launch from the two counter passes of
 # profiles/gemm_head_nt_8192x8192x512_traffic.md: FETCH_SIZE 108751.9 KiB × 2.000
 # + WRITE_SIZE 262156.3 KiB × 1.000 (factors from the 256 MiB copy).
-HEAD_TRAFFIC_BYTES = (108751.9 * 2.000 + 262156.3 * 1.000) * 1024
+HEAD_TRAFFIC_BYTES = (156261.9 * 2.000 + 262144.4 * 1.000) * 1024
 SWEEP_KN = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
 M = 8192
 
