@@ -727,14 +727,8 @@ __global__ void __launch_bounds__(256, 5) mha_bwd_dq_direct_kernel(AttnArgs a) {
   load_ds(0, fc);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  for (int kt = 0; kt <= qt; ++kt) {
-    const bool more = kt < qt;
-    if (more) {  // the other buffer was released by the previous barrier
-      issue_k(kt + 1, sm[(kt + 1) & 1]);
-      load_ds(kt + 1, fn);
-    }
-    const float* Ks = sm[kt & 1];
-    const int jmax = more ? 3 : w;
+  // acc += dS(tile)·K(tile) over this wave's sub-tiles j ≤ jmax
+  auto tile_mfma = [&](const float* Ks, int jmax) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (j > jmax) continue;
@@ -748,13 +742,36 @@ __global__ void __launch_bounds__(256, 5) mha_bwd_dq_direct_kernel(AttnArgs a) {
         }
       }
     }
-    if (more) {
+  };
+  // Key tiles below the diagonal: a branch-free body, in which the next
+  // tile's 8 loads (4 K granule rows straight into LDS, 4 dS fragments) are
+  // spread among the first MFMAs and the K fragment reads (one b32 per MFMA)
+  // run two ahead of their MFMAs (sched_group_barrier classes: 0x008 MFMA,
+  // 0x020 VMEM read, 0x100 DS read).  Measured on MI355X at C2: backward
+  // 0.406-0.408 → 0.400-0.402 ms against the compiler's own schedule.
+  for (int kt = 0; kt < qt; ++kt) {
+    // the other buffer was released by the previous barrier
+    issue_k(kt + 1, sm[(kt + 1) & 1]);
+    load_ds(kt + 1, fn);
+    tile_mfma(sm[kt & 1], 3);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) fc[j] = fn[j];
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
+    for (int r = 0; r < 8; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
+#pragma unroll
+    for (int r = 0; r < 24; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fc[j] = fn[j];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
   }
+  tile_mfma(sm[qt & 1], w);  // the diagonal tile: sub-tiles j ≤ w
   const int qrow = qt * TQ + 16 * w + l16;
   if (qrow < a.T) {
     float* dqr = a.dq + (row_base + qrow) * a.ld_d + h * DH;
