@@ -78,15 +78,20 @@ template <int DH>
 struct TileRegs {
   using G = Geo<DH>;
   floatx4 v[G::NV];
-  __device__ __forceinline__ void load(const float* __restrict__ base, int ld, int r0, int T,
+  int r0 = 0, T = 0;  // of the last load: rows r0 + r ≥ T are stored as zeros
+  // Branch-free, and nothing consumes the loaded values before store(): a
+  // row past T is read from row T − 1 (in range) and zeroed only when stored,
+  // so the loads stay in flight under whatever runs in between.
+  __device__ __forceinline__ void load(const float* __restrict__ base, int ld, int r0_, int T_,
                                        int tid) {
+    r0 = r0_;
+    T = T_;
 #pragma unroll
     for (int i = 0; i < G::NV; ++i) {
       const int f = tid + i * 256;
       const int r = f / (DH / 4), c = (f % (DH / 4)) * 4;
-      floatx4 x = {0.f, 0.f, 0.f, 0.f};
-      if (f < G::F4 && r0 + r < T) x = *reinterpret_cast<const floatx4*>(base + (size_t)(r0 + r) * ld + c);
-      v[i] = x;
+      if (G::F4 % 256 == 0 || f < G::F4)
+        v[i] = *reinterpret_cast<const floatx4*>(base + (size_t)min(r0 + r, T - 1) * ld + c);
     }
   }
   __device__ __forceinline__ void store(float* __restrict__ s, int tid) const {
@@ -94,7 +99,10 @@ struct TileRegs {
     for (int i = 0; i < G::NV; ++i) {
       const int f = tid + i * 256;
       const int r = f / (DH / 4), c = (f % (DH / 4)) * 4;
-      if (f < G::F4) *reinterpret_cast<floatx4*>(s + r * G::LDT + c) = v[i];
+      if (G::F4 % 256 == 0 || f < G::F4) {
+        const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<floatx4*>(s + r * G::LDT + c) = r0 + r < T ? v[i] : zero;
+      }
     }
   }
 };
@@ -480,12 +488,17 @@ __global__ void __launch_bounds__(256, (NS == 1 ? 3 : 1)) mha_bwd_dkv_kernel(Att
     zero_pad_cols<DH>(sm[st][1], tid);
   }
   TileRegs<DH> rq, rd;
+  // The next tile's row statistics, raw: scaled and masked only when stored,
+  // so no wait for them (and, the load counter being in order, for the
+  // tile loads before them) at the top of the tile.
   float r_lse = 0.f, r_D = 0.f;
+  int r_q = 0;
   auto load_stats = [&](int q0) {
     if (tid < TQ) {
-      const int q = q0 + tid;
-      r_lse = q < a.T ? a.lse[stat + q] * LOG2E : 0.f;
-      r_D = q < a.T ? a.D[stat + q] : 0.f;
+      r_q = q0 + tid;
+      const int qc = min(r_q, a.T - 1);
+      r_lse = a.lse[stat + qc];
+      r_D = a.D[stat + qc];
     }
   };
   rq.load(Qb, a.ld_qkv, k0, a.T, tid);
@@ -494,8 +507,8 @@ __global__ void __launch_bounds__(256, (NS == 1 ? 3 : 1)) mha_bwd_dkv_kernel(Att
   rq.store(sm[0][0], tid);
   rd.store(sm[0][1], tid);
   if (tid < TQ) {
-    st_lse[0][tid] = r_lse;
-    st_D[0][tid] = r_D;
+    st_lse[0][tid] = r_q < a.T ? r_lse * LOG2E : 0.f;
+    st_D[0][tid] = r_q < a.T ? r_D : 0.f;
   }
   __syncthreads();
 
@@ -563,8 +576,8 @@ __global__ void __launch_bounds__(256, (NS == 1 ? 3 : 1)) mha_bwd_dkv_kernel(Att
       rq.store(sm[(cur + 1) % NS][0], tid);
       rd.store(sm[(cur + 1) % NS][1], tid);
       if (tid < TQ) {
-        st_lse[(cur + 1) % NS][tid] = r_lse;
-        st_D[(cur + 1) % NS][tid] = r_D;
+        st_lse[(cur + 1) % NS][tid] = r_q < a.T ? r_lse * LOG2E : 0.f;
+        st_D[(cur + 1) % NS][tid] = r_q < a.T ? r_D : 0.f;
       }
     }
     __syncthreads();
