@@ -22,8 +22,8 @@
 // computed transposed (Sᵀ = K·Qᵀ), which leaves lane l holding column l%16
 // of Sᵀ — all of them scores of ONE query row — so the softmax statistics
 // are per-lane scalars and the Sᵀ accumulator registers are directly the
-// B operand of the next product (Oᵀ = Vᵀ·Pᵀ).  The row max is reduced over
-// the four 16-lane groups with cross-lane swizzles (shfl_xor 16, 32).
+// B operand of the next product (Oᵀ = Vᵀ·Pᵀ).  The row max and sum are
+// reduced over the four 16-lane groups with gfx950's row-swap permutes.
 // The head dimension is covered in chunks of 16 (NC = ceil(DH/16)); when
 // DH is not a multiple of 16 the last chunk's upper half (8 columns) is zero.
 #include "common.hpp"
@@ -59,6 +59,29 @@ struct AttnArgs {
 };
 
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// Max and sum over lanes l, l^16, l^32, l^48 (the four 16-lane rows), every
+// lane getting the result.  v_permlane16_swap exchanges the odd rows of its
+// first operand with the even rows of its second (v_permlane32_swap: the
+// upper half with the lower half), so with both operands = v each lane ends
+// up holding its own value and its partner row's: VALU only, no LDS round
+// trip as with a bpermute.  Sums add (r0 + r1) + (r2 + r3) in every lane.
+__device__ __forceinline__ float rows4_max(float v) {
+  const unsigned u = __float_as_uint(v);
+  auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+  const unsigned u2 = __float_as_uint(v);
+  auto t = __builtin_amdgcn_permlane32_swap(u2, u2, false, false);
+  return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+__device__ __forceinline__ float rows4_sum(float v) {
+  const unsigned u = __float_as_uint(v);
+  auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  const unsigned u2 = __float_as_uint(v);
+  auto t = __builtin_amdgcn_permlane32_swap(u2, u2, false, false);
+  return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
 
 template <int DH>
 struct Geo {
@@ -170,8 +193,7 @@ __device__ __forceinline__ void fwd_tile(const float* __restrict__ Ks, const flo
   float mx = fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3]));
 #pragma unroll
   for (int j = 1; j < 4; ++j) mx = fmaxf(mx, fmaxf(fmaxf(st[j][0], st[j][1]), fmaxf(st[j][2], st[j][3])));
-  mx = fmaxf(mx, shfl_xor(mx, 16));
-  mx = fmaxf(mx, shfl_xor(mx, 32));
+  mx = rows4_max(mx);
   const float m_new = fmaxf(m, mx);
   const float alpha = __builtin_amdgcn_exp2f(m - m_new);
   m = m_new;
@@ -254,8 +276,7 @@ __global__ void __launch_bounds__(256) mha_fwd_kernel(AttnArgs a) {
   }
   fwd_tile<DH, true>(sm[0], sm[1], qf, acc_o, m, l, w, g, l16);
 
-  l += shfl_xor(l, 16);
-  l += shfl_xor(l, 32);
+  l = rows4_sum(l);
   if (qrow < a.T) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
     float* orow = a.out + (row_base + qrow) * a.ld_o + h * DH;
@@ -271,16 +292,19 @@ __global__ void __launch_bounds__(256) mha_fwd_kernel(AttnArgs a) {
 // into LDS with global_load_lds_dwordx4 (a wave instruction fills 1 KB = four
 // 64-float rows): no staging registers and no ds_write.  One LDS stage
 // (32 KB), so that as many blocks share a CU as with the register-staged
-// kernel; a block's next-tile load latency is covered by the other blocks.
-// The rows are unpadded; XOR swizzles of the 16-byte granules keep the
-// fragment reads conflict-free:
-//   K (b128 reads of 16 consecutive rows at one granule): granule q of row r at q ^ (r & 15);
-//   V (b32 reads of rows 4g + s, 16 consecutive columns):  q ^ (((r >> 2) & 3) << 2).
+// kernel; a block's next-tile load latency is covered by the other blocks
+// (loading K and V half a tile apart, each behind the other half's compute,
+// measured no faster on MI355X at C2: 0.147 ms both).
+// The rows are unpadded.  K fragments are b128 reads of 16 consecutive rows
+// at one granule, kept conflict-free by an XOR swizzle of the 16-byte
+// granules (granule q of row r at q ^ (r & 15)); V fragments are b128 reads
+// in which each group of 16 lanes reads one whole row, conflict-free as laid
+// out.
 // Rows past T are loaded from row T − 1 (finite, and masked: a key ≥ T is
 // always in the future of every query < T).
 template <bool ISK>
 __device__ __forceinline__ int attn_swz(int row, int q) {
-  return ISK ? q ^ (row & 15) : q ^ (((row >> 2) & 3) << 2);
+  return ISK ? q ^ (row & 15) : q;
 }
 
 template <bool ISK>
@@ -297,13 +321,12 @@ __device__ __forceinline__ void issue_kv64(const float* __restrict__ base, int l
   }
 }
 
+// Sᵀ of one 64-key tile against the wave's 16 queries (K from LDS).
 template <bool DIAG>
-__device__ __forceinline__ void fwd_tile_direct(const float* __restrict__ Ks, const float* __restrict__ Vs,
-                                                const floatx4* qf, floatx4* acc_o, float& m, float& l,
-                                                int w, int g, int l16) {
+__device__ __forceinline__ void fwd_scores_direct(const float* __restrict__ Ks, const floatx4* qf, floatx4* st,
+                                                  int w, int g, int l16) {
   constexpr int NC = 4;
   const int jmax = DIAG ? w : 3;
-  floatx4 st[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     st[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -324,11 +347,18 @@ __device__ __forceinline__ void fwd_tile_direct(const float* __restrict__ Ks, co
       for (int e = 0; e < 4; ++e)
         if (j > jmax || 16 * j + 4 * g + e > 16 * w + l16) st[j][e] = -INFINITY;
   }
+}
+
+// Online softmax of the tile's scores, then O += P·V (V from LDS).
+template <bool DIAG>
+__device__ __forceinline__ void fwd_pv_direct(const float* __restrict__ Vs, floatx4* st, floatx4* acc_o, float& m,
+                                              float& l, int w, int g, int l16) {
+  constexpr int NC = 4;
+  const int jmax = DIAG ? w : 3;
   float mx = fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3]));
 #pragma unroll
   for (int j = 1; j < 4; ++j) mx = fmaxf(mx, fmaxf(fmaxf(st[j][0], st[j][1]), fmaxf(st[j][2], st[j][3])));
-  mx = fmaxf(mx, shfl_xor(mx, 16));
-  mx = fmaxf(mx, shfl_xor(mx, 32));
+  mx = rows4_max(mx);
   const float m_new = fmaxf(m, mx);
   const float alpha = __builtin_amdgcn_exp2f(m - m_new);
   m = m_new;
@@ -349,13 +379,12 @@ __device__ __forceinline__ void fwd_tile_direct(const float* __restrict__ Ks, co
     if (j <= jmax) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
+        // Oᵀ tile d holds the columns 4·r + d (r = 0..15): one b128 read of
+        // V[key][4·l16 .. 4·l16 + 3] feeds the four tiles.
         const int key = 16 * j + 4 * g + s;
+        const floatx4 v = *reinterpret_cast<const floatx4*>(Vs + key * 64 + 4 * attn_swz<false>(key, l16));
 #pragma unroll
-        for (int d = 0; d < NC; ++d) {
-          const int col = 16 * d + l16;
-          const float v = Vs[key * 64 + 4 * attn_swz<false>(key, col >> 2) + (col & 3)];
-          acc_o[d] = mfma16x16x4(v, st[j][s], acc_o[d]);
-        }
+        for (int d = 0; d < NC; ++d) acc_o[d] = mfma16x16x4(v[d], st[j][s], acc_o[d]);
       }
     }
   }
@@ -389,22 +418,27 @@ __global__ void __launch_bounds__(256, 4) mha_fwd_direct_kernel(AttnArgs a) {
   for (int d = 0; d < NC; ++d) acc_o[d] = floatx4{0.f, 0.f, 0.f, 0.f};
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  floatx4 st[4];
   for (int kt = 0; kt < qt; ++kt) {
-    fwd_tile_direct<false>(sm[0], sm[1], qf, acc_o, m, l, w, g, l16);
+    fwd_scores_direct<false>(sm[0], qf, st, w, g, l16);
+    fwd_pv_direct<false>(sm[1], st, acc_o, m, l, w, g, l16);
     __syncthreads();  // every wave is done with the stage
     issue_kv64<true>(Kb, a.ld_qkv, (kt + 1) * TQ, a.T, sm[0], w, lane);
     issue_kv64<false>(Vb, a.ld_qkv, (kt + 1) * TQ, a.T, sm[1], w, lane);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
-  fwd_tile_direct<true>(sm[0], sm[1], qf, acc_o, m, l, w, g, l16);
-  l += shfl_xor(l, 16);
-  l += shfl_xor(l, 32);
+  fwd_scores_direct<true>(sm[0], qf, st, w, g, l16);
+  fwd_pv_direct<true>(sm[1], st, acc_o, m, l, w, g, l16);
+  l = rows4_sum(l);
   if (qrow < a.T) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
     float* orow = a.out + (row_base + qrow) * a.ld_o + h * DH;
+    // acc_o[d][i] is O[qrow][16·g + 4·i + d]
 #pragma unroll
-    for (int d = 0; d < NC; ++d) *reinterpret_cast<floatx4*>(orow + 16 * d + 4 * g) = acc_o[d] * inv;
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<floatx4*>(orow + 16 * g + 4 * i) =
+          floatx4{acc_o[0][i], acc_o[1][i], acc_o[2][i], acc_o[3][i]} * inv;
     if (g == 0) a.lse[((size_t)b * a.H + h) * a.T + qrow] = (m + __log2f(l)) * (1.f / LOG2E);
   }
 }
