@@ -10,25 +10,40 @@
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
+#include <type_traits>
 
 namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr int kChains = 8;  // independent accumulators per wave
 
+// WIDE = false: v_mfma_f32_16x16x4_f32 (2048 FLOP, the form the GEMM and
+// attention kernels use); true: v_mfma_f32_32x32x2_f32 (4096 FLOP).
+template <bool WIDE>
 __global__ void __launch_bounds__(256) mfma_f32_peak_kernel(int iters, float* sink) {
+  using acc_t = typename std::conditional<WIDE, floatx16, floatx4>::type;
+  constexpr int NE = WIDE ? 16 : 4;
   const float a = 1.0f + 1e-3f * (threadIdx.x & 7), b = 1.0f - 1e-3f * (threadIdx.x & 3);
-  floatx4 acc[kChains];
+  acc_t acc[kChains];
 #pragma unroll
-  for (int j = 0; j < kChains; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < kChains; ++j)
+#pragma unroll
+    for (int e = 0; e < NE; ++e) acc[j][e] = 0.f;
   for (int i = 0; i < iters; ++i) {  // 4 rounds of the chains per trip
 #pragma unroll
-    for (int r = 0; r < 4 * kChains; ++r)
-      acc[r % kChains] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[r % kChains], 0, 0, 0);
+    for (int r = 0; r < 4 * kChains; ++r) {
+      if constexpr (WIDE)
+        acc[r % kChains] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[r % kChains], 0, 0, 0);
+      else
+        acc[r % kChains] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[r % kChains], 0, 0, 0);
+    }
   }
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < kChains; ++j) s += (acc[j][0] + acc[j][1]) + (acc[j][2] + acc[j][3]);
+  for (int j = 0; j < kChains; ++j)
+#pragma unroll
+    for (int e = 0; e < NE; ++e) s += acc[j][e];
   sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
@@ -65,7 +80,18 @@ double ceil_mfma_f32_flop(int blocks, int iters) {
 // sink: blocks · 256 floats of device memory.
 int ceil_mfma_f32(void* stream, int blocks, int iters, float* sink) {
   if (blocks <= 0 || iters <= 0 || !sink) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(mfma_f32_peak_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, iters, sink);
+  hipLaunchKernelGGL(mfma_f32_peak_kernel<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, iters, sink);
+  return (int)hipGetLastError();
+}
+
+// The same probe with v_mfma_f32_32x32x2_f32: blocks · 4 · iters · 4 · chains · 2·32·32·2 FLOP.
+double ceil_mfma_f32_32x32_flop(int blocks, int iters) {
+  return (double)blocks * 4.0 * iters * 4 * kChains * 4096.0;
+}
+
+int ceil_mfma_f32_32x32(void* stream, int blocks, int iters, float* sink) {
+  if (blocks <= 0 || iters <= 0 || !sink) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(mfma_f32_peak_kernel<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, iters, sink);
   return (int)hipGetLastError();
 }
 

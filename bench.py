@@ -199,6 +199,9 @@ def bench_ceilings(ctx, cus: int) -> dict:
     lib.ceil_mfma_f32_flop.restype = C.c_double
     lib.ceil_mfma_f32_flop.argtypes = [C.c_int, C.c_int]
     lib.ceil_mfma_f32.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+    lib.ceil_mfma_f32_32x32_flop.restype = C.c_double
+    lib.ceil_mfma_f32_32x32_flop.argtypes = [C.c_int, C.c_int]
+    lib.ceil_mfma_f32_32x32.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
     lib.ceil_stream_read.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_void_p]
     lib.ceil_graph_create.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_void_p)]
     lib.ceil_graph_launch.argtypes = [C.c_void_p, C.c_void_p]
@@ -217,6 +220,10 @@ def bench_ceilings(ctx, cus: int) -> dict:
         ctx.sync()
     ms = time_region(ctx, lambda: ok(lib.ceil_mfma_f32(stream, mfma_blocks, iters, sink.ptr), "ceil_mfma_f32"), 5)
     mfma_tf = lib.ceil_mfma_f32_flop(mfma_blocks, iters) / (ms * 1e-3) / 1e12
+    # the 32x32x2 form, same FLOP per launch (half the iterations)
+    ms32 = time_region(ctx, lambda: ok(lib.ceil_mfma_f32_32x32(stream, mfma_blocks, iters // 2, sink.ptr),
+                                        "ceil_mfma_f32_32x32"), 5)
+    mfma32_tf = lib.ceil_mfma_f32_32x32_flop(mfma_blocks, iters // 2) / (ms32 * 1e-3) / 1e12
 
     nbytes = 2 << 30
     src = GpuBuffer.zeros(ctx, nbytes // 4)
@@ -244,10 +251,12 @@ def bench_ceilings(ctx, cus: int) -> dict:
     ok(lib.ceil_graph_destroy(ex), "ceil_graph_destroy")
     sink.free()
     out = {"mfma_fp32_tflops": round(mfma_tf, 1), "mfma_fp32_frac_of_peak": round(mfma_tf / PEAK_FP32_MFMA, 3),
+           "mfma_fp32_32x32x2_tflops": round(mfma32_tf, 1),
            "hbm_read_gbs": round(read_gbs, 1), "hbm_read_frac_of_peak": round(read_gbs / PEAK_HBM, 3),
            "hbm_read_best": best, "hbm_read_all_gbs": {k: round(v, 1) for k, v in reads.items()},
            "graph_empty_kernel_us": round(ms_g * 1e3 / n_launch, 2),
-           "probes": "register-operand fp32 MFMA (16x16x4), 2 GiB streaming read, empty kernel in a HIP graph"}
+           "probes": "register-operand fp32 MFMA (16x16x4, and 32x32x2), 2 GiB streaming read, "
+                     "empty kernel in a HIP graph"}
     log(f"[bench] ceilings {out}")
     return out
 

@@ -77,12 +77,15 @@ def test_ceiling_probe_library_loads():
     from aurora_amd.build import PROBE_LIB
 
     lib = C.CDLL(str(PROBE_LIB))
-    for name in ("ceil_mfma_f32", "ceil_mfma_f32_flop", "ceil_stream_read", "ceil_graph_create",
-                 "ceil_graph_launch", "ceil_graph_destroy"):
+    for name in ("ceil_mfma_f32", "ceil_mfma_f32_flop", "ceil_mfma_f32_32x32", "ceil_mfma_f32_32x32_flop",
+                 "ceil_stream_read", "ceil_graph_create", "ceil_graph_launch", "ceil_graph_destroy"):
         assert hasattr(lib, name), name
     lib.ceil_mfma_f32_flop.restype = C.c_double
     lib.ceil_mfma_f32_flop.argtypes = [C.c_int, C.c_int]
     assert lib.ceil_mfma_f32_flop(512, 10) == 512 * 4 * 10 * 4 * 8 * 2048
+    lib.ceil_mfma_f32_32x32_flop.restype = C.c_double
+    lib.ceil_mfma_f32_32x32_flop.argtypes = [C.c_int, C.c_int]
+    assert lib.ceil_mfma_f32_32x32_flop(512, 5) == lib.ceil_mfma_f32_flop(512, 10)
 
 
 def test_kernel_structs_refuse_short_buffers():
