@@ -38,6 +38,64 @@ constexpr float LOG2E = 1.4426950408889634f;
 
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// Cross-lane exchange without the LDS round trip of a bpermute: the value
+// of lane (this lane ^ M), M a power of two ≤ 32.  M = 1, 2 are DPP
+// quad_perm moves; M = 16, 32 the row-swap permutes (v_permlane16_swap swaps
+// the odd rows of its first operand with the even rows of its second,
+// v_permlane32_swap the upper half with the lower half, so with both
+// operands = v one result holds this lane's value and the other its
+// partner's).  For M = 4, 8 the exact exchange is a bpermute, unless
+// UNIFORM: the value is the same on every lane of each aligned group of M
+// lanes, and then row_half_mirror (lane ^ 7) and row_mirror (lane ^ 15)
+// read a lane holding the partner's value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int M, bool UNIFORM>
+__device__ __forceinline__ float lane_xor(float v) {
+  if constexpr (M == 1) {
+    return dpp_mov<0xB1>(v);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (M == 2) {
+    return dpp_mov<0x4E>(v);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (M == 4 && UNIFORM) {
+    return dpp_mov<0x141>(v);  // row_half_mirror
+  } else if constexpr (M == 8 && UNIFORM) {
+    return dpp_mov<0x140>(v);  // row_mirror
+  } else if constexpr (M == 16 || M == 32) {
+    const unsigned u = __float_as_uint(v);
+    const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float((threadIdx.x & M) ? r[0] : r[1]);
+  } else {
+    return shfl_xor(v, M);
+  }
+}
+// Σ / max over each aligned group of G lanes, from groups of S lanes whose
+// values are uniform (S = 1: none are), as the butterfly v ∘= v(lane ^ M)
+// for M = S, 2S, … < G, every lane adding its own value first.
+// Σ over lanes l, l ^ S, l ^ 2S, … (the same position in every group of S
+// lanes), for values that differ between the lanes of a group.
+template <int S>
+__device__ __forceinline__ float group_sum_lanes(float v) {
+  if constexpr (S < 64) {
+    v += lane_xor<S, false>(v);
+    return group_sum_lanes<2 * S>(v);
+  } else {
+    return v;
+  }
+}
+template <int S, int G, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+  if constexpr (S < G) {
+    const float o = lane_xor<S, true>(v);
+    v = MAX ? fmaxf(v, o) : v + o;
+    return group_reduce<2 * S, G, MAX>(v);
+  } else {
+    return v;
+  }
+}
+
 struct KvArgs {
   const float* q;       // [B, ld_q] rows, head h at h*d_head
   const float* kh;      // [B, max_len, ld]
@@ -281,14 +339,12 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float s = qv[0] * kc[u][0] + qv[1] * kc[u][1] + qv[2] * kc[u][2] + qv[3] * kc[u][3];
-#pragma unroll
-      for (int o = LPK / 2; o >= 1; o >>= 1) s += shfl_xor(s, o);
+      s = group_reduce<1, LPK, false>(s);  // the key's LPK lanes
       if (base + (u * SW + w) * KPS + g >= T) s = -INFINITY;
       sc[u] = s;
       mx = fmaxf(mx, s);
     }
-#pragma unroll
-    for (int o = LPK; o < 64; o <<= 1) mx = fmaxf(mx, shfl_xor(mx, o));
+    mx = group_reduce<LPK, 64, true>(mx);  // uniform over each key's LPK lanes
     const float m_new = fmaxf(m, mx);
     if (m_new != -INFINITY) {  // wave-uniform: some key of this wave so far
       const float alpha = exp2f(m - m_new);
@@ -308,13 +364,11 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
       vc[u] = vn[u];
     }
   }
-  // Sum the lane groups (each group holds its own keys' l and acc).
+  // Sum the lane groups (each group holds its own keys' l and acc; l is
+  // uniform over a group's lanes, acc is not: it holds the lane's dims).
+  l = group_reduce<LPK, 64, false>(l);
 #pragma unroll
-  for (int o = LPK; o < 64; o <<= 1) {
-    l += shfl_xor(l, o);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] += shfl_xor(acc[i], o);
-  }
+  for (int i = 0; i < 4; ++i) acc[i] = group_sum_lanes<LPK>(acc[i]);
   if (g == 0 && live) *reinterpret_cast<floatx4*>(&wo[w][4 * part]) = acc;
   if (lane == 0) {
     wm[w] = m;
