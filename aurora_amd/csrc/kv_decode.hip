@@ -206,9 +206,7 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
     }
 #pragma unroll
     for (int it = 0; it < KPW / KPS; ++it) {
-      float s = s_loc[it];
-#pragma unroll
-      for (int m = LPK / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
+      const float s = group_reduce<1, LPK, false>(s_loc[it]);  // the key's LPK lanes
       const int kl = w * KPW + KPS * it + g;
       if (part == 0) sc[kl] = (c0 + kl < T) ? s : -INFINITY;
     }
@@ -216,7 +214,7 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
 
     // Chunk max and exp-sum (log2 domain).
     float v = tid < KC ? sc[tid] : -INFINITY;
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, shfl_xor(v, o));
+    v = group_reduce<1, 64, true>(v);
     if (lane == 0) red[w] = v;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -227,7 +225,7 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
       sc[tid] = e;
     }
     float sum = e;
-    for (int o = 32; o >= 1; o >>= 1) sum += shfl_xor(sum, o);
+    sum = group_reduce<1, 64, false>(sum);
     if (lane == 0) red[w] = sum;
     __syncthreads();
     const float L = (red[0] + red[1]) + (red[2] + red[3]);
@@ -240,9 +238,7 @@ __global__ void __launch_bounds__(256) kv_chunk_kernel(KvArgs a) {
       acc += sc[kl] * vreg[it];  // sc = 0 for keys >= T (exp2(-inf))
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int m = LPK; m < 64; m <<= 1) acc[i] += shfl_xor(acc[i], m);
+    for (int i = 0; i < 4; ++i) acc[i] = group_sum_lanes<LPK>(acc[i]);
     if (g == 0 && live) *reinterpret_cast<floatx4*>(&obuf[w][4 * part]) = acc;
     __syncthreads();
     if (tid < DH) {
