@@ -381,14 +381,14 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(GemmArgs g) {
 //     two groups, so every granule stays in its row.
 // The swizzle is an involution, so the same function maps physical → logical
 // on the load side.
-template <int ROWS, bool KCONTIG, int BK = 32>
+template <int ROWS, bool KCONTIG, int BK = 32, int NWV = 4>
 struct DirectTile {
   static_assert(BK == 32 || BK == 16, "BK is 16 or 32");
   static constexpr int ELEMS = ROWS * BK;
   static constexpr int GPR = KCONTIG ? BK / 4 : ROWS / 4;  // 16-byte granules per LDS row
   static constexpr int RPI = 64 / GPR;                     // LDS rows per wave instruction
-  static constexpr int NIW = (KCONTIG ? ROWS : BK) / RPI / 4;  // instructions per wave
-  static_assert(NIW >= 1 && (KCONTIG ? ROWS : BK) % (RPI * 4) == 0, "tile too small for four waves");
+  static constexpr int NIW = (KCONTIG ? ROWS : BK) / RPI / NWV;  // instructions per wave
+  static_assert(NIW >= 1 && (KCONTIG ? ROWS : BK) % (RPI * NWV) == 0, "tile too small for the waves");
 
   static_assert(KCONTIG || GPR >= 8, "the k-strided swizzle needs at least 8 granules per LDS row");
   __device__ static __forceinline__ int phys(int lrow, int q) {
@@ -437,16 +437,17 @@ struct DirectTile {
 // beside the fragments in the 256 registers of two waves per SIMD.  Its waves
 // each own 128×64 outputs: 6 load instructions per 128 MFMAs instead of 8,
 // and 12 fragment reads per 32 MFMAs instead of 8 per 16.
-template <int BM, int BN, bool AK, bool BKC, int PRE = 0, int BK = 32>
-__global__ void __launch_bounds__(kThreads, (BM == 256 ? 2 : 1)) gemm_f32_mfma_direct(GemmArgs g) {
+template <int BM, int BN, bool AK, bool BKC, int PRE = 0, int BK = 32, int NW = 4>
+__global__ void __launch_bounds__(64 * NW, (BM == 256 || NW == 8 ? 2 : 1)) gemm_f32_mfma_direct(GemmArgs g) {
   select_batch(g);
-  using TA = DirectTile<BM, AK, BK>;
-  using TB = DirectTile<BN, BKC, BK>;
+  using TA = DirectTile<BM, AK, BK, NW>;
+  using TB = DirectTile<BN, BKC, BK, NW>;
   constexpr int ST = TA::ELEMS + TB::ELEMS;
-  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
+  constexpr int WGN = NW / 2;  // waves along N (two along M)
+  constexpr int WM = BM / 2, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
   __shared__ __attribute__((aligned(1024))) float smem[2 * ST];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int g16 = lane >> 4, l16 = lane & 15;
   // Tile order: as gemm_f32_mfma (contiguous run per XCD, 8-row groups).
   constexpr int GM = 8;
@@ -1038,8 +1039,14 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int 
   return p;
 }
 
+// cus: the device's CU count (0: unknown).  A 128×128 grid of at most one
+// block per CU runs the 8-wave kernel (each wave 64×32 of the tile): one
+// block then puts two waves on every SIMD, which cover each other's barrier
+// and LDS waits (measured on MI355X: 8192×512×512 114.6 → 118.1 TFLOP/s,
+// 8192×512×2048 130.6 → 134.8; on grids of two or more blocks per CU the
+// 4-wave kernel is 1-2 % faster).
 template <int BM, int BN, bool AK, bool BKC>
-void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int batch) {
+void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int batch, int cus) {
   dim3 grid(a.tiles_m * a.tiles_n, batch, splits);
   if constexpr (BM == 256) {  // whole tiles only: the planner's allow_wide condition
     hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, 0, 16>), grid, dim3(kThreads), 0, st, a);
@@ -1047,6 +1054,12 @@ void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int ba
   const bool whole = vec && a.M % BM == 0 && a.N % BN == 0 && a.K % 32 == 0 && a.k_chunk % 32 == 0;
   if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr) {
     if constexpr (BM == 128 && BN == 128) {
+      const long blocks = (long)a.tiles_m * a.tiles_n * batch * splits;
+      if (cus > 0 && blocks <= cus &&
+          (a.split || a.epi.mode == aur::EPI_STORE || a.epi.mode == aur::EPI_ACCUM)) {
+        hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, 0, 32, 8>), grid, dim3(512), 0, st, a);
+        return;
+      }
       if (!a.split && a.epi.mode == aur::EPI_RESID) {
         hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, aur::EPI_RESID>), grid, dim3(kThreads), 0,
                            st, a);
@@ -1068,20 +1081,20 @@ void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int ba
 }
 
 template <bool AK, bool BKC>
-void launch_layout(const GemmArgs& a, const Plan& p, bool vec, hipStream_t st, int batch = 1) {
+void launch_layout(const GemmArgs& a, const Plan& p, bool vec, hipStream_t st, int cus, int batch = 1) {
   if constexpr (AK) {
-    if (p.bm == 256) return launch_tile<256, 128, AK, BKC>(a, p.splits, vec, st, batch);
+    if (p.bm == 256) return launch_tile<256, 128, AK, BKC>(a, p.splits, vec, st, batch, cus);
   }
   if (p.bm == 128 && p.bn == 128)
-    launch_tile<128, 128, AK, BKC>(a, p.splits, vec, st, batch);
+    launch_tile<128, 128, AK, BKC>(a, p.splits, vec, st, batch, cus);
   else if (p.bm == 128 && p.bn == 64)
-    launch_tile<128, 64, AK, BKC>(a, p.splits, vec, st, batch);
+    launch_tile<128, 64, AK, BKC>(a, p.splits, vec, st, batch, cus);
   else if (p.bm == 64 && p.bn == 64)
-    launch_tile<64, 64, AK, BKC>(a, p.splits, vec, st, batch);
+    launch_tile<64, 64, AK, BKC>(a, p.splits, vec, st, batch, cus);
   else if (p.bm == 64 && p.bn == 32)
-    launch_tile<64, 32, AK, BKC>(a, p.splits, vec, st, batch);
+    launch_tile<64, 32, AK, BKC>(a, p.splits, vec, st, batch, cus);
   else
-    launch_tile<32, 32, AK, BKC>(a, p.splits, vec, st, batch);
+    launch_tile<32, 32, AK, BKC>(a, p.splits, vec, st, batch, cus);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -1263,13 +1276,13 @@ int gemm(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, int lda, 
     a.split = 1;
   }
   if (a_kcontig && b_kcontig)
-    launch_layout<true, true>(a, p, vec, ctx->stream);
+    launch_layout<true, true>(a, p, vec, ctx->stream, ctx->cu_count);
   else if (a_kcontig && !b_kcontig)
-    launch_layout<true, false>(a, p, vec, ctx->stream);
+    launch_layout<true, false>(a, p, vec, ctx->stream, ctx->cu_count);
   else if (!a_kcontig && b_kcontig)
-    launch_layout<false, true>(a, p, vec, ctx->stream);
+    launch_layout<false, true>(a, p, vec, ctx->stream, ctx->cu_count);
   else
-    launch_layout<false, false>(a, p, vec, ctx->stream);
+    launch_layout<false, false>(a, p, vec, ctx->stream, ctx->cu_count);
   AUR_LAUNCH_CHECK(ctx, "gemm_f32_mfma");
   if (p.splits > 1) {
     reduce_partials(ctx, a.P, C, M, N, ldc, p.splits, epi);
@@ -1306,13 +1319,13 @@ int gemm_batched(aur_ctx* ctx, bool a_kcontig, bool b_kcontig, const float* A, i
   a.k_chunk = p.k_chunk;
   a.sA = sA; a.sB = sB; a.sC = sC;
   if (a_kcontig && b_kcontig)
-    launch_layout<true, true>(a, p, vec, ctx->stream, batch);
+    launch_layout<true, true>(a, p, vec, ctx->stream, ctx->cu_count, batch);
   else if (a_kcontig && !b_kcontig)
-    launch_layout<true, false>(a, p, vec, ctx->stream, batch);
+    launch_layout<true, false>(a, p, vec, ctx->stream, ctx->cu_count, batch);
   else if (!a_kcontig && b_kcontig)
-    launch_layout<false, true>(a, p, vec, ctx->stream, batch);
+    launch_layout<false, true>(a, p, vec, ctx->stream, ctx->cu_count, batch);
   else
-    launch_layout<false, false>(a, p, vec, ctx->stream, batch);
+    launch_layout<false, false>(a, p, vec, ctx->stream, ctx->cu_count, batch);
   AUR_LAUNCH_CHECK(ctx, "gemm_f32_mfma (batched)");
   return 0;
 }
