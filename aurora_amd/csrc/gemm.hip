@@ -1039,12 +1039,13 @@ Plan choose_plan(const aur_ctx* ctx, int M, int N, int K, bool allow_split, int 
   return p;
 }
 
-// cus: the device's CU count (0: unknown).  A 128×128 grid of at most one
-// block per CU runs the 8-wave kernel (each wave 64×32 of the tile): one
-// block then puts two waves on every SIMD, which cover each other's barrier
-// and LDS waits (measured on MI355X: 8192×512×512 114.6 → 118.1 TFLOP/s,
-// 8192×512×2048 130.6 → 134.8; on grids of two or more blocks per CU the
-// 4-wave kernel is 1-2 % faster).
+// cus: the device's CU count (0: unknown).  A 128×128 or 128×64 grid of at
+// most one block per CU runs the 8-wave kernel (each wave 64×32 or 64×16 of
+// the tile): one block then puts two waves on every SIMD, which cover each
+// other's barrier and LDS waits (measured on MI355X: 8192×512×512 114.6 →
+// 118.1 TFLOP/s, 8192×512×2048 130.6 → 134.8, 2048×1024×4096 with 128×64
+// tiles 2-3 % faster; on grids of two or more blocks per CU the 4-wave
+// kernel is 1-2 % faster).
 template <int BM, int BN, bool AK, bool BKC>
 void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int batch, int cus) {
   dim3 grid(a.tiles_m * a.tiles_n, batch, splits);
@@ -1053,13 +1054,15 @@ void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int ba
   } else {
   const bool whole = vec && a.M % BM == 0 && a.N % BN == 0 && a.K % 32 == 0 && a.k_chunk % 32 == 0;
   if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr) {
-    if constexpr (BM == 128 && BN == 128) {
+    if constexpr (BM == 128 && (BN == 128 || BN == 64)) {
       const long blocks = (long)a.tiles_m * a.tiles_n * batch * splits;
       if (cus > 0 && blocks <= cus &&
           (a.split || a.epi.mode == aur::EPI_STORE || a.epi.mode == aur::EPI_ACCUM)) {
         hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, 0, 32, 8>), grid, dim3(512), 0, st, a);
         return;
       }
+    }
+    if constexpr (BM == 128 && BN == 128) {
       if (!a.split && a.epi.mode == aur::EPI_RESID) {
         hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, aur::EPI_RESID>), grid, dim3(kThreads), 0,
                            st, a);
