@@ -1056,7 +1056,7 @@ void launch_tile(const GemmArgs& a, int splits, bool vec, hipStream_t st, int ba
   if (whole && std::getenv("AUR_GEMM_STAGED") == nullptr) {
     if constexpr (BM == 128 && (BN == 128 || BN == 64)) {
       const long blocks = (long)a.tiles_m * a.tiles_n * batch * splits;
-      if (cus > 0 && blocks <= cus &&
+      if (cus > 0 && blocks <= cus && std::getenv("AUR_GEMM_NO_W8") == nullptr &&
           (a.split || a.epi.mode == aur::EPI_STORE || a.epi.mode == aur::EPI_ACCUM)) {
         hipLaunchKernelGGL((gemm_f32_mfma_direct<BM, BN, AK, BKC, 0, 32, 8>), grid, dim3(512), 0, st, a);
         return;

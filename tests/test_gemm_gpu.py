@@ -334,6 +334,27 @@ def test_nt_equals_nn_on_materialised_transpose(ctx):
     assert fro_rel(nt, nn) < 1e-6
 
 
+@pytest.mark.parametrize("form,m,n,k,cfg", [("nt", 8192, 512, 512, "128x128:1"), ("nn", 8192, 512, 1024, "128x128:1"),
+                                            ("nt", 2048, 1024, 1024, "128x64:1"), ("acc", 2048, 512, 1024, "128x128:4")])
+def test_eight_wave_kernel_bitwise_equals_four_wave(ctx, monkeypatch, form, m, n, k, cfg):
+    """A 128×128 or 128×64 grid of at most one block per CU (here 256 blocks,
+    the MI355X's CU count; split-K included) runs 8 waves per block.  Every
+    output is summed in the same order as by the 4-wave kernel, so the two
+    agree bit for bit; AUR_GEMM_NO_W8 keeps the 4-wave kernel."""
+    rng = np.random.default_rng(m + n + k)
+    monkeypatch.setenv("AUR_GEMM_CFG", cfg)
+    if form == "acc":  # dest[m, n] += Σ_t dY[t, m]·X[t, n], t = k
+        x, dy, dest = _u(rng, k * n), _u(rng, k * m), _u(rng, m * n)
+        run = lambda: _outer(ctx, x, dy, dest, m, n, k)
+    else:
+        a, b = _u(rng, m * k), _u(rng, k * n)
+        run = lambda: (_nt if form == "nt" else _nn)(ctx, a, b, m, n, k)
+    eight = run()
+    monkeypatch.setenv("AUR_GEMM_NO_W8", "1")
+    four = run()
+    np.testing.assert_array_equal(eight, four)
+
+
 def test_split_k_refused_while_captured(ctx, monkeypatch):
     """A split-K GEMM enqueued while the library's stream is being captured
     into a HIP graph, without a caller workspace, is refused (the graph would
