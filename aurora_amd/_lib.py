@@ -71,8 +71,8 @@ SIGNATURES: dict[str, tuple] = {
                                              C.POINTER(C.c_float)]),
     "aur_model_grad_norm": (_i32, [C.c_void_p, C.POINTER(C.c_float)]),
     "aur_model_state_bytes": (_i32, [C.c_void_p, C.POINTER(C.c_size_t)]),
-    "aur_model_state_save": (_i32, [C.c_void_p, C.c_void_p, C.POINTER(C.c_uint64)]),
-    "aur_model_state_load": (_i32, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    "aur_model_state_save": (_i32, [C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_uint64)]),
+    "aur_model_state_load": (_i32, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint64]),
     "aur_model_forward": (_i32, [C.c_void_p, C.c_void_p, _u32, _u32, C.c_void_p]),
     "aur_model_eval_step_batch": (_i32, [C.c_void_p, C.c_void_p, C.c_void_p, _u32, _u32,
                                          C.c_void_p]),

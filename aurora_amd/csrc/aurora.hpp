@@ -293,13 +293,15 @@ class DecoderTransformerGpu {
   float clip_grads_adamw_subset(float max_norm, bool want_norm = true);
 
   // snapshot_state / refresh_state / restore_state (src/gpu/transformer.rs:
-  // 1152-1240): the persistent state — parameters, both AdamW moments and,
-  // once allocated, the Muon momentum — as one device-to-device copy into or
-  // out of a caller-owned buffer of state_bytes() bytes.  The optimizer step
-  // counter travels separately (`step`).
+  // 1152-1240): the persistent state — parameters, both AdamW moments and
+  // the Muon momentum (allocated with the model, as the reference's mu
+  // buffers are, so the size never changes) — copied device-to-device into
+  // or out of a caller-owned buffer of `bytes` bytes, which must equal
+  // state_bytes() (AUR_EINVAL otherwise).  The optimizer step counter
+  // travels separately (`step`).
   size_t state_bytes() const;
-  void copy_state_to(void* dst) const;
-  void copy_state_from(const void* src);
+  void copy_state_to(void* dst, size_t bytes) const;
+  void copy_state_from(const void* src, size_t bytes);
 
   // Zero the optimizer state (AdamW moments, Muon momentum) — a fresh optimizer.
   void reset_optimizer_state();
@@ -380,6 +382,10 @@ class KvCacheGpu {
   size_t part_floats_ = 0;
   int qkv_parts = 1;  // K ranges of the decode QKV projection held in qkv_
   int o_parts = 1, p_parts = 1;  // K ranges of the W_o / W_proj products in part_
+  // W_o / W_proj as K-range partials summed by the following LayerNorm
+  // (batch <= 64 and d_model <= 4096, the row-resident LayerNorm kernels'
+  // limit); otherwise whole products with the residual fused.
+  bool split = false;
   size_t bytes_ = 0;
   void* graph_ = nullptr;       // hipGraphExec_t of one decode step, built on first use
 };

@@ -1127,6 +1127,7 @@ void noalloc_scratch_init(aur_ctx* ctx) {
   const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
   if (e != hipSuccess || ptr == nullptr) {
     ctx->noalloc_err = e != hipSuccess ? (int)e : AUR_ENOMEM;
+    (void)hipGetLastError();  // keep the failure from being reported by the next launch check
     return;
   }
   per_device[ctx->device] = static_cast<float*>(ptr);

@@ -133,12 +133,19 @@ void DecoderTransformerGpu::init() {
   // ones (w_pos, per layer ln1_g, ln1_b, ln2_g, ln2_b, then lnf_g, lnf_b).
   n_decay_ = V * d + L * (3 * d * d + d * d + F * d + d * F);
   n_params_ = n_decay_ + Tm * d + L * 4 * d + 2 * d;
-  ck(ctx_, aur_malloc(ctx_, 4 * n_params_ * sizeof(float) + 4096, &state_mem_), "alloc params");
+  // params | grads | m1 | m2 | Muon momentum (one float per matrix
+  // parameter, [V·d, n_decay) of the flat layout).  The momentum exists from
+  // the start, as the reference's GpuParams mu buffers do, so the persistent
+  // state (and state_bytes()) has one fixed size.
+  const size_t n_mu = n_decay_ - V * d;
+  const size_t state_floats = 4 * n_params_ + n_mu;
+  ck(ctx_, aur_malloc(ctx_, state_floats * sizeof(float) + 4096, &state_mem_), "alloc params");
   params_ = static_cast<float*>(state_mem_);
   grads_ = params_ + n_params_;
   m1_ = grads_ + n_params_;
   m2_ = m1_ + n_params_;
-  ck(ctx_, aur_memset0(ctx_, state_mem_, 4 * n_params_ * sizeof(float)), "zero state");
+  mu_ = m2_ + n_params_;
+  ck(ctx_, aur_memset0(ctx_, state_mem_, state_floats * sizeof(float)), "zero state");
 
   layers_ = new std::vector<Layer>(L);
   acts_ = new Acts();
@@ -526,8 +533,8 @@ inline float powi_f(float b, uint64_t e) {
 
 void DecoderTransformerGpu::reset_optimizer_state() {
   ck(ctx_, aur_memset0(ctx_, m1_, 2 * n_params_ * sizeof(float)), "zero moments");
-  if (mu_) ck(ctx_, aur_memset0(ctx_, mu_, (n_decay_ - (size_t)cfg_.vocab * cfg_.d_model) * sizeof(float)),
-              "zero muon momentum");
+  ck(ctx_, aur_memset0(ctx_, mu_, (n_decay_ - (size_t)cfg_.vocab * cfg_.d_model) * sizeof(float)),
+     "zero muon momentum");
 }
 
 // ------------------------------------------------------------------ Muon
@@ -574,13 +581,11 @@ void DecoderTransformerGpu::step_muon_hybrid(const MuonConfig& mc, const AdamWCo
   }
   const size_t m_ff = std::min(d, F), n_ff = std::max(d, F);
   if (!muon_mem_) {
-    const size_t n_mat = n_decay_ - n_tok;
     const size_t xs = std::max(sq.size() * d * d, ff.size() * m_ff * n_ff);
     const size_t as = std::max(sq.size() * d * d, ff.size() * m_ff * m_ff);
-    const size_t floats = n_mat + 3 * xs + 3 * as + 64;
-    ck(ctx_, aur_malloc(ctx_, floats * sizeof(float) + 8 * 256, &muon_mem_), "alloc muon state");
+    const size_t floats = 3 * xs + 3 * as + 64;
+    ck(ctx_, aur_malloc(ctx_, floats * sizeof(float) + 8 * 256, &muon_mem_), "alloc muon scratch");
     Carver cv{static_cast<char*>(muon_mem_)};
-    mu_ = cv.take<float>(n_mat);
     ns_x_[0] = cv.take<float>(xs);
     ns_x_[1] = cv.take<float>(xs);
     ns_bx_ = cv.take<float>(xs);
@@ -588,7 +593,6 @@ void DecoderTransformerGpu::step_muon_hybrid(const MuonConfig& mc, const AdamWCo
     ns_a2_ = cv.take<float>(as);
     ns_b_ = cv.take<float>(as);
     muon_stats_ = cv.take<float>(64);
-    ck(ctx_, aur_memset0(ctx_, mu_, n_mat * sizeof(float)), "zero muon momentum");
   }
   // model.rs:1031-1032: one shared step counter for the AdamW bias correction.
   step += 1;
@@ -678,30 +682,29 @@ float DecoderTransformerGpu::clip_and_step_adamw(float max_norm, const AdamWConf
 }
 
 // ------------------------------------------------------------ state snapshot
-// params | m1 | m2 are contiguous thirds of state_mem_ apart from grads, so
-// the copy is three device-to-device copies, plus the Muon momentum.
+// params, then m1 | m2 | Muon momentum, which lie contiguously in
+// state_mem_ after the gradients: two device-to-device copies.  The size is
+// fixed for the model's lifetime (the momentum is allocated with it).
 size_t DecoderTransformerGpu::state_bytes() const {
-  const size_t mom = mu_ ? (n_decay_ - (size_t)cfg_.vocab * cfg_.d_model) : 0;
-  return (3 * n_params_ + mom) * sizeof(float);
+  return (3 * n_params_ + (n_decay_ - (size_t)cfg_.vocab * cfg_.d_model)) * sizeof(float);
 }
 
-void DecoderTransformerGpu::copy_state_to(void* dst) const {
+void DecoderTransformerGpu::copy_state_to(void* dst, size_t bytes) const {
   if (!dst) throw Error("copy_state_to: null buffer", AUR_EINVAL);
+  if (bytes != state_bytes()) throw Error("copy_state_to: buffer size differs from state_bytes()", AUR_EINVAL);
   float* d = static_cast<float*>(dst);
   const size_t n = n_params_ * sizeof(float);
   ck(ctx_, aur_d2d(ctx_, d, params_, n), "snapshot params");
-  ck(ctx_, aur_d2d(ctx_, d + n_params_, m1_, 2 * n), "snapshot moments");
-  if (mu_)
-    ck(ctx_, aur_d2d(ctx_, d + 3 * n_params_, mu_, state_bytes() - 3 * n), "snapshot muon momentum");
+  ck(ctx_, aur_d2d(ctx_, d + n_params_, m1_, bytes - n), "snapshot moments + muon momentum");
 }
 
-void DecoderTransformerGpu::copy_state_from(const void* src) {
+void DecoderTransformerGpu::copy_state_from(const void* src, size_t bytes) {
   if (!src) throw Error("copy_state_from: null buffer", AUR_EINVAL);
+  if (bytes != state_bytes()) throw Error("copy_state_from: buffer size differs from state_bytes()", AUR_EINVAL);
   const float* s = static_cast<const float*>(src);
   const size_t n = n_params_ * sizeof(float);
   ck(ctx_, aur_d2d(ctx_, params_, s, n), "restore params");
-  ck(ctx_, aur_d2d(ctx_, m1_, s + n_params_, 2 * n), "restore moments");
-  if (mu_) ck(ctx_, aur_d2d(ctx_, mu_, s + 3 * n_params_, state_bytes() - 3 * n), "restore muon momentum");
+  ck(ctx_, aur_d2d(ctx_, m1_, s + n_params_, bytes - n), "restore moments + muon momentum");
 }
 
 // ------------------------------------------------------------------ KV cache
@@ -715,7 +718,8 @@ KvCacheGpu::KvCacheGpu(DecoderTransformerGpu& model, uint32_t batch_, uint32_t m
   const size_t B = batch, d = d_model, F = c.d_ff, V = c.vocab;
   const size_t hist = (size_t)n_layer * B * max_len * d;
   const size_t scratch = (aur_mha_kv_ws_bytes(batch, c.n_head, max_len) + 3) / 4;
-  if (batch <= 64) {
+  split = batch <= 64 && d <= 4096;
+  if (split) {
     // The decode QKV projection as qkv_parts K-range partials [parts][B][3d]
     // that the attention kernel sums; W_o / W_proj as K-range partials
     // [splits][B][d] that the following LayerNorm sums.
@@ -867,13 +871,22 @@ void DecoderTransformerGpu::encode_decode_step(KvCacheGpu& cache) {
   // with B ≤ 64 rows they are split into K ranges whose partial products the
   // following LayerNorm sums (with the residual add) — more blocks in flight
   // and no separate reduction launch.
-  const bool split = cache.batch <= 64;
+  const bool split = cache.split;
   const int s_o = cache.o_parts, s_p = cache.p_parts;
   // h = w_tok[tok] + w_pos[pos]  (kv_cache.rs:103-115), lens = pos + 1 for
-  // the attention below, and the first block's LayerNorm of h
-  ck(ctx_, aur::embed_layer_norm(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, cache.x_, (*layers_)[0].ln1_g,
-                                 (*layers_)[0].ln1_b, cache.ln_, cache.lens_, B, d, kLnEps),
-     "embed + ln1");
+  // the attention below, and the first block's LayerNorm of h (one launch
+  // up to the row-resident kernel's d <= 4096, else two)
+  if (d <= 4096) {
+    ck(ctx_, aur::embed_layer_norm(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, cache.x_,
+                                   (*layers_)[0].ln1_g, (*layers_)[0].ln1_b, cache.ln_, cache.lens_, B, d, kLnEps),
+       "embed + ln1");
+  } else {
+    ck(ctx_, aur::embed_forward(ctx_, A.w_tok, A.w_pos, cache.tok_, cache.pos_, 1, cache.x_, B, d, cache.lens_),
+       "embed");
+    ck(ctx_, aur::layer_norm_forward(ctx_, cache.x_, (*layers_)[0].ln1_g, (*layers_)[0].ln1_b, cache.ln_, nullptr,
+                                     nullptr, B, d, kLnEps),
+       "ln1");
+  }
   // Attention is launched for lengths up to max_len (keys past a sequence's
   // length are skipped on the device), so the launch shape is the same for
   // every step.
@@ -1086,18 +1099,18 @@ int aur_model_state_bytes(aur_model* m, size_t* bytes) {
   return 0;
 }
 
-int aur_model_state_save(aur_model* m, void* dst, uint64_t* step) {
+int aur_model_state_save(aur_model* m, void* dst, size_t bytes, uint64_t* step) {
   if (!m || !dst) return AUR_EINVAL;
   return guard(m->m->ctx(), [&] {
-    m->m->copy_state_to(dst);
+    m->m->copy_state_to(dst, bytes);
     if (step) *step = m->m->step;
   });
 }
 
-int aur_model_state_load(aur_model* m, const void* src, uint64_t step) {
+int aur_model_state_load(aur_model* m, const void* src, size_t bytes, uint64_t step) {
   if (!m || !src) return AUR_EINVAL;
   return guard(m->m->ctx(), [&] {
-    m->m->copy_state_from(src);
+    m->m->copy_state_from(src, bytes);
     m->m->step = step;
   });
 }

@@ -158,11 +158,11 @@ class DecoderTransformerGpu:
 
     def refresh_state(self, buf) -> None:
         st = C.c_uint64()
-        self._call("aur_model_state_save", buf.ptr, C.byref(st))
+        self._call("aur_model_state_save", buf.ptr, buf.nbytes, C.byref(st))
         buf.step = st.value
 
     def restore_state(self, buf) -> None:
-        self._call("aur_model_state_load", buf.ptr, buf.step)
+        self._call("aur_model_state_load", buf.ptr, buf.nbytes, buf.step)
 
     def forward(self, tokens, want_logits: bool = True):
         tok = _u32(tokens)

@@ -296,13 +296,16 @@ int aur_model_clip_grads_adamw_subset(aur_model* m, float max_norm, float* norm)
 int aur_model_clip_step_adamw(aur_model* m, float max_norm, float lr, float beta1, float beta2,
                               float eps, float weight_decay, float* norm);
 /* snapshot_state / refresh_state / restore_state (transformer.rs:1152-1240):
- * the persistent state — parameters, both AdamW moments and, once allocated,
- * the Muon momentum — copied device-to-device into / out of a caller-owned
- * DEVICE buffer of aur_model_state_bytes bytes (enqueued, no host sync);
- * the optimizer step counter is returned / set alongside. */
+ * the persistent state — parameters, both AdamW moments and the Muon
+ * momentum (allocated with the model, like the reference's mu buffers, so
+ * the size is fixed for the model's lifetime) — copied device-to-device into
+ * / out of a caller-owned DEVICE buffer of `bytes` bytes (enqueued, no host
+ * sync); `bytes` must equal aur_model_state_bytes, else AUR_EINVAL and
+ * nothing is copied.  The optimizer step counter is returned / set
+ * alongside. */
 int aur_model_state_bytes(aur_model* m, size_t* bytes);
-int aur_model_state_save(aur_model* m, void* dst, uint64_t* step);
-int aur_model_state_load(aur_model* m, const void* src, uint64_t step);
+int aur_model_state_save(aur_model* m, void* dst, size_t bytes, uint64_t* step);
+int aur_model_state_load(aur_model* m, const void* src, size_t bytes, uint64_t step);
 
 /* KvCacheGpu::new (kv_cache.rs:42) for `batch` sequences decoded together,
  * max_len <= seq_len_max; reset zeroes it (kv_cache.rs:76).  A cache serves

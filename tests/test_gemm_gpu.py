@@ -334,13 +334,20 @@ def test_nt_equals_nn_on_materialised_transpose(ctx):
     assert fro_rel(nt, nn) < 1e-6
 
 
-@pytest.mark.parametrize("form,m,n,k,cfg", [("nt", 8192, 512, 512, "128x128:1"), ("nn", 8192, 512, 1024, "128x128:1"),
-                                            ("nt", 2048, 1024, 1024, "128x64:1"), ("acc", 2048, 512, 1024, "128x128:4")])
-def test_eight_wave_kernel_bitwise_equals_four_wave(ctx, monkeypatch, form, m, n, k, cfg):
-    """A 128×128 or 128×64 grid of at most one block per CU (here 256 blocks,
-    the MI355X's CU count; split-K included) runs 8 waves per block.  Every
-    output is summed in the same order as by the 4-wave kernel, so the two
-    agree bit for bit; AUR_GEMM_NO_W8 keeps the 4-wave kernel."""
+@pytest.mark.parametrize("form,n,k,cfg,splits", [("nt", 512, 512, "128x128:1", 1), ("nn", 512, 1024, "128x128:1", 1),
+                                                ("nt", 1024, 1024, "128x64:1", 1), ("acc", 512, 1024, "128x128:4", 4)])
+def test_eight_wave_kernel_bitwise_equals_four_wave(ctx, monkeypatch, form, n, k, cfg, splits):
+    """A 128×128 or 128×64 grid of at most one block per CU (split-K
+    included) runs 8 waves per block.  Every output is summed in the same
+    order as by the 4-wave kernel, so the two agree bit for bit;
+    AUR_GEMM_NO_W8 keeps the 4-wave kernel.  m is chosen from the device's
+    CU count so that the grid has exactly one block per CU (256 on MI355X)."""
+    _, cus = ctx.device_info()
+    bn = int(cfg.split("x")[1].split(":")[0])
+    col_tiles = n // bn
+    if cus % (col_tiles * splits) != 0:
+        pytest.skip(f"{cus} CUs: no m gives one {cfg} block per CU at n = {n}")
+    m = 128 * (cus // (col_tiles * splits))
     rng = np.random.default_rng(m + n + k)
     monkeypatch.setenv("AUR_GEMM_CFG", cfg)
     if form == "acc":  # dest[m, n] += Σ_t dY[t, m]·X[t, n], t = k

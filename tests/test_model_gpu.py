@@ -232,6 +232,40 @@ def test_grad_norm_snapshot_and_optional_norm(ctx):
     m.destroy()
 
 
+def test_state_snapshot_size_fixed_across_muon(ctx):
+    """The persistent state has one size for the model's lifetime: a snapshot
+    taken before the first Muon step (whose momentum the reference keeps in
+    its mu buffers from the start) still fits after it, round-trips the
+    momentum, and a buffer of any other size is refused before any copy."""
+    from aurora_amd._lib import AuroraError
+    from aurora_amd.gpu import GpuBuffer
+    cfg = C0
+    P = OM.init_params(cfg, 7)
+    tok, tgt = _tokens(cfg, 2, 64, 7)
+    m = _gpu_model(ctx, cfg, 2, P)
+    n0 = m.state_bytes()
+    snap = m.snapshot_state()
+    m.zero_grad()
+    m.train_step_batch(tok, tgt)
+    m.step_muon_hybrid()
+    assert m.state_bytes() == n0
+    m.refresh_state(snap)
+    after_one = snap.download()
+    m.zero_grad()
+    m.train_step_batch(tok, tgt)
+    m.step_muon_hybrid()
+    assert not np.array_equal(m.snapshot_state().download(), after_one)
+    m.restore_state(snap)
+    assert np.array_equal(m.snapshot_state().download(), after_one)
+    short = GpuBuffer.empty(ctx, n0 // 4 - 1)
+    for bad in (lambda: m.refresh_state(short), lambda: m.restore_state(short)):
+        short.step = 0
+        with pytest.raises(AuroraError):
+            bad()
+    assert np.array_equal(m.snapshot_state().download(), after_one)
+    m.destroy()
+
+
 def test_kv_cache_belongs_to_its_model(ctx):
     """A cache's captured decode step holds its model's weight pointers: a
     second model may not use it, and once its model is destroyed the cache
