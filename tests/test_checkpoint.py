@@ -72,6 +72,60 @@ def test_restatement_roundtrip_and_size(tmp_path):
     np.testing.assert_array_equal(np.frombuffer(raw[-32:], "<f4"), P["lnf_b"])
 
 
+# Every tensor of an AURORA07 file with every optional feature off, in the
+# order of the layout comment at checkpoint.rs:27-49 (and `save` :145-186):
+# (name, layer, element count).  Written out here, not taken from the
+# restatement's own tensor order, so that the two pin each other.
+TWO = OM.Config(vocab=12, d_model=16, n_layer=2, n_head=2, d_ff=20, seq_len_max=6)
+
+
+def _layout_table(cfg):
+    d, F = cfg.d_model, cfg.d_ff
+    rows = [("w_tok", -1, cfg.vocab * d), ("w_pos", -1, cfg.seq_len_max * d)]
+    for l in range(cfg.n_layer):
+        rows += [("ln1_g", l, d), ("ln1_b", l, d), ("w_q", l, d * d), ("w_k", l, d * d), ("w_v", l, d * d),
+                 ("w_o", l, d * d), ("ln2_g", l, d), ("ln2_b", l, d), ("w_fc", l, F * d), ("w_proj", l, d * F)]
+    rows += [("lnf_g", -1, d), ("lnf_b", -1, d)]
+    return rows
+
+
+def _tagged_params(cfg):
+    """Each tensor filled with its own index in the table × 1000 + position,
+    so any tensor read at another's offset is detected."""
+    P = OM.init_params(cfg, 0)
+    for i, (name, l, n) in enumerate(_layout_table(cfg)):
+        a = P[name] if l < 0 else P["layers"][l][name]
+        assert a.size == n, (name, l)
+        a[...] = (1000.0 * (i + 1) + np.arange(n, dtype=np.float32)).reshape(a.shape)
+    return P
+
+
+def _check_offsets(raw, cfg):
+    off = 60  # the V7 header (test_v7_header_byte_layout)
+    for i, (name, l, n) in enumerate(_layout_table(cfg)):
+        got = np.frombuffer(raw[off:off + 4 * n], "<f4")
+        np.testing.assert_array_equal(got, 1000.0 * (i + 1) + np.arange(n, dtype=np.float32),
+                                      err_msg=f"{name}[{l}] at byte {off}")
+        off += 4 * n
+    assert off == len(raw)
+
+
+def test_two_layer_tensor_offsets(tmp_path):
+    """Byte offset of every per-block tensor of a 2-layer AURORA07 file
+    (checkpoint.rs:27-49): the restatement writes each tensor where the
+    layout table puts it, and reads each back from there."""
+    P = _tagged_params(TWO)
+    CK.write(tmp_path / "two.ckpt", TWO, P)
+    _check_offsets((tmp_path / "two.ckpt").read_bytes(), TWO)
+    # a file assembled byte by byte from the table reads back tensor by tensor
+    body = b"".join((1000.0 * (i + 1) + np.arange(n, dtype=np.float32)).astype("<f4").tobytes()
+                    for i, (_, _, n) in enumerate(_layout_table(TWO)))
+    (tmp_path / "hand.ckpt").write_bytes(CK.header_bytes(TWO, 0, 0) + body)
+    _, Q = CK.read(tmp_path / "hand.ckpt")
+    for (name, l, a), (_, _, b) in zip(OM.tensors(P), OM.tensors(Q)):
+        np.testing.assert_array_equal(a, b, err_msg=f"{name}[{l}]")
+
+
 @pytest.mark.parametrize("version", [5, 6, 7])
 def test_peek_through_c_abi(tmp_path, version):
     from aurora_amd.model import peek_checkpoint
@@ -124,6 +178,33 @@ def test_gpu_save_read_by_restatement(ctx, tmp_path):
     for (name, l, a), (_, _, b) in zip(OM.tensors(P), OM.tensors(Q)):
         np.testing.assert_array_equal(a, b, err_msg=f"{name}[{l}]")
     m.destroy()
+
+
+@pytest.mark.gpu
+def test_gpu_save_two_layer_offsets_and_hand_built_load(ctx, tmp_path):
+    """The C++ writer puts every tensor of a 2-layer model at the offset of
+    the layout table (checkpoint.rs:27-49), and the C++ reader takes each
+    tensor of a file assembled byte by byte from that table."""
+    from aurora_amd.model import DecoderTransformerGpu
+
+    P = _tagged_params(TWO)
+    m = _gpu_model(ctx, TWO, 1)
+    m.load_params(P)
+    path = tmp_path / "two_gpu.ckpt"
+    m.save_checkpoint(path, epoch=0, step=0)
+    _check_offsets(path.read_bytes(), TWO)
+    m.destroy()
+    hand = tmp_path / "hand.ckpt"
+    body = b"".join((1000.0 * (i + 1) + np.arange(n, dtype=np.float32)).astype("<f4").tobytes()
+                    for i, (_, _, n) in enumerate(_layout_table(TWO)))
+    hand.write_bytes(CK.header_bytes(TWO, 0, 0) + body)
+    g = DecoderTransformerGpu.from_checkpoint(ctx, hand, max_batch=1)
+    Q = g.read_tensors(grad=False)
+    for i, (name, l, n) in enumerate(_layout_table(TWO)):
+        got = Q[name] if l < 0 else Q["layers"][l][name]
+        np.testing.assert_array_equal(np.ravel(got), 1000.0 * (i + 1) + np.arange(n, dtype=np.float32),
+                                      err_msg=f"{name}[{l}]")
+    g.destroy()
 
 
 @pytest.mark.gpu

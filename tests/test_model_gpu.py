@@ -576,3 +576,55 @@ def test_kv_cache_starts_zeroed_and_reset_matches_fresh(ctx):
     for c in (fresh, dirty):
         c.destroy()
     m.destroy()
+
+
+def test_gpu_model_matches_torch_definition(ctx):
+    """The GPU model against the tiny pre-LN GPT written from torch
+    primitives (tests/golden/model_fixture.npz, float64, independent of the
+    CPU oracle): logits, per-sequence losses, every gradient of the batch
+    mean, one clip + AdamW step with the reference's decay groups, and two
+    Muon hybrid steps after the AdamW-subset clip."""
+    from pathlib import Path
+    fx = np.load(Path(__file__).resolve().parent / "golden" / "model_fixture.npz", allow_pickle=False)
+    cfg = OM.Config(*(int(v) for v in fx["cfg"]))
+
+    def tree(prefix):
+        P = {k: fx[f"{prefix}.{k}"].astype(np.float32) for k in ("w_tok", "w_pos", "lnf_g", "lnf_b")}
+        P["layers"] = [{k: fx[f"{prefix}.l{l}.{k}"].astype(np.float32) for k in OM.LAYER_KEYS}
+                       for l in range(cfg.n_layer)]
+        return P
+
+    tok, tgt = fx["tokens"], fx["targets"]
+    B, T = tok.shape
+    P0 = tree("p")
+    m = _gpu_model(ctx, cfg, B, P0)
+    logits = m.forward(tok).reshape(B, T, cfg.vocab)
+    assert fro_rel(logits, fx["logits"]) < 1e-5
+    m.zero_grad()
+    loss = m.train_step_batch(tok, tgt)
+    assert abs(loss - fx["seq_loss"].sum()) < 1e-5 * fx["seq_loss"].sum()
+    _compare_tree(m.read_tensors(grad=True), tree("g"), 1e-4, "grad vs torch")
+    snap = m.snapshot_state()
+    norm = m.clip_grads(float(fx["clip_max_norm"]))
+    assert abs(norm - float(fx["grad_norm"])) < 1e-5 * norm
+    m.step_adamw(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    got = m.read_tensors(grad=False)
+    for (name, l, g), (_, _, w), (_, _, p) in zip(OM.tensors(got), OM.tensors(tree("adamw")), OM.tensors(P0)):
+        step, want = g.astype(np.float64) - p.ravel(), w.ravel() - p.ravel().astype(np.float64)
+        assert np.max(np.abs(step - want)) < 2e-7 * max(1.0, np.max(np.abs(p))) + 3e-7, (name, l)
+    # Muon hybrid from the same gradients and a fresh optimizer state
+    m.restore_state(snap)
+    m.zero_grad()
+    m.train_step_batch(tok, tgt)
+    sub = m.clip_grads_adamw_subset(float(fx["subset_max_norm"]))
+    assert abs(sub - float(fx["subset_norm"])) < 1e-5 * sub
+    prev = P0
+    for step in (1, 2):
+        m.step_muon_hybrid()
+        got = m.read_tensors(grad=False)
+        want = tree(f"muon{step}")
+        for (name, l, g), (_, _, w), (_, _, p) in zip(OM.tensors(got), OM.tensors(want), OM.tensors(prev)):
+            upd = g.astype(np.float64) - p.ravel()
+            assert fro_rel(upd, w.ravel() - p.ravel().astype(np.float64)) < 1e-3, (step, name, l)
+        prev = got
+    m.destroy()

@@ -19,6 +19,9 @@ Parity status per oracle function — every one is pinned:
   embed_forward/backward ................................ closed form
   kv_attend ........................... last row of sdpa_forward
   model forward/backward ........ central differences + the above
+  model assembly (block wiring, batch mean, clip + AdamW decay groups,
+  AdamW-subset norm, Muon hybrid rows × cols) ..... torch float64 tiny GPT
+                                 from primitives (tests/golden/model_fixture.npz)
   generate_step ...................... full forward (last row)
 """
 from pathlib import Path
@@ -295,3 +298,91 @@ def test_embed_refuses_positions_past_the_table():
     with pytest.raises(ValueError):
         O.embed_forward(np.zeros((5, 4), np.float32), np.zeros((3, 4), np.float32),
                         np.zeros(4, np.uint32), 4)
+
+
+# ------------------------------------- model assembly vs the torch fixture
+# tests/golden/model_fixture.npz holds a tiny pre-LN GPT written from torch
+# primitives alone (tests/golden/make_fixtures.py), independent of oracle/:
+# its forward wiring, autograd gradients, clip + AdamW with the reference's
+# decay groups and the Muon hybrid step pin how oracle/model.py assembles the
+# primitives that the tests above pin one by one.
+MFX = np.load(Path(__file__).resolve().parent / "golden" / "model_fixture.npz", allow_pickle=False)
+MCFG = OM.Config(*(int(v) for v in MFX["cfg"]))
+
+
+def _fixture_tree(prefix):
+    """A fixture's flat 'l{l}.key' arrays as the oracle's parameter dict."""
+    P = {k: MFX[f"{prefix}.{k}"].astype(np.float32).copy() for k in ("w_tok", "w_pos", "lnf_g", "lnf_b")}
+    P["layers"] = [{k: MFX[f"{prefix}.l{l}.{k}"].astype(np.float32).copy() for k in OM.LAYER_KEYS}
+                   for l in range(MCFG.n_layer)]
+    return P
+
+
+def _pairs(A, prefix):
+    for name, l, a in OM.tensors(A):
+        key = name if l < 0 else f"l{l}.{name}"
+        yield key, a, MFX[f"{prefix}.{key}"]
+
+
+def test_model_forward_matches_torch_definition():
+    """Logits and per-sequence mean NLL of the oracle's forward equal the
+    torch model's (pre-LN blocks, LN2 on the post-attention residual, final
+    LN, tied head)."""
+    P = _fixture_tree("p")
+    V = MCFG.vocab
+    for b in range(MFX["tokens"].shape[0]):
+        logits, _ = OM.forward(P, MCFG, MFX["tokens"][b])
+        assert rel(logits, MFX["logits"][b]) < 2e-6, b
+        total, _ = O.softmax_ce(logits, MFX["targets"][b], V)
+        assert abs(total / MFX["targets"].shape[1] - MFX["seq_loss"][b]) < 2e-6 * MFX["seq_loss"][b]
+
+
+def test_model_batch_grads_match_torch_autograd():
+    P = _fixture_tree("p")
+    loss, G = OM.batch_grads(P, MCFG, MFX["tokens"], MFX["targets"])
+    assert abs(loss - MFX["seq_loss"].sum()) < 1e-5
+    n = 0
+    for key, g, want in _pairs(G, "g"):
+        assert rel(g, want) < 2e-5, key
+        n += 1
+    assert n == 4 + 10 * MCFG.n_layer
+    # rows of w_pos past t get no gradient
+    assert not np.any(G["w_pos"][MFX["tokens"].shape[1]:])
+
+
+def test_clip_and_adamw_match_torch_with_reference_decay_groups():
+    """clip_grads (model.rs:1011-1017) at half the norm, then one step_adamw:
+    w_tok, w_q/k/v/o, w_fc, w_proj decayed; w_pos and LayerNorm γ/β not."""
+    P = _fixture_tree("p")
+    G = _fixture_tree("g")
+    n = OM.clip_grads(G, float(MFX["clip_max_norm"]))
+    assert abs(n - float(MFX["grad_norm"])) < 1e-5 * n
+    OM.step_adamw(P, G, OM.new_adam_state(P), lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.1)
+    p0 = _fixture_tree("p")
+    for (key, p, want), (_, _, start) in zip(_pairs(P, "adamw"), _pairs(p0, "p")):
+        # compare the step itself: parameters move by ~lr, fp32 keeps ~1e-7·|θ|
+        step, want_step = p.astype(np.float64) - start, want - start.astype(np.float64)
+        assert np.max(np.abs(step - want_step)) < 2e-7 * max(1.0, np.max(np.abs(start))) + 1e-3 * 3e-4, key
+
+
+def test_muon_hybrid_matches_torch_definition():
+    """clip_grads_adamw_subset (model.rs:1101-1107; the norm over the subset
+    of model.rs:518-560) and two step_muon_hybrid calls with the same
+    gradients (AdamW on the subset, Muon with the reference's rows × cols
+    on the block matrices) against the torch float64 restatement."""
+    P = _fixture_tree("p")
+    G = _fixture_tree("g")
+    n = OM.clip_grads_adamw_subset(G, float(MFX["subset_max_norm"]))
+    assert abs(n - float(MFX["subset_norm"])) < 1e-5 * n
+    adam, muon = OM.new_adam_state(P), OM.new_muon_state(P)
+    prev = _fixture_tree("p")
+    for step in (1, 2):
+        OM.step_muon_hybrid(P, G, adam, muon, MCFG)
+        for (key, p, want), (_, _, before) in zip(_pairs(P, f"muon{step}"), _pairs(prev, "p" if step == 1 else
+                                                                                  f"muon{step - 1}")):
+            upd = p.astype(np.float64) - before.astype(np.float64)
+            want_upd = want - before.astype(np.float64)
+            # Muon moves a matrix by lr·√(max/min)·(orthogonalised update):
+            # compare the update; AdamW entries move by ~lr
+            assert rel(upd, want_upd) < 2e-4, (step, key)
+        prev = OM.copy_params(P)
