@@ -715,6 +715,13 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 // Workspace: rowdot D [B,H,T], padded to 256 bytes, then the dS tiles.
 size_t ws_d_floats(size_t b, size_t t, size_t n_head) { return (b * t * n_head + 63) / 64 * 64; }
 
+// Floats of that layout: D plus every 64×64 tile of the causal lower
+// triangle, ≈ b·n_head·t²/2 for long sequences.
+size_t tiled_ws_floats(size_t b, size_t t, size_t n_head) {
+  const size_t nqt = (t + TQ - 1) / TQ;
+  return ws_d_floats(b, t, n_head) + b * n_head * (nqt * (nqt + 1) / 2) * TQ * TQ;
+}
+
 bool dh_supported(uint32_t d) { return d >= 8 && d <= 64 && d % 8 == 0; }
 
 int check_common(aur_ctx* ctx, uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head,
@@ -863,10 +870,16 @@ void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
 
 // overwrite = 0: dq/dk/dv += (the C ABI's contract); 1: dq/dk/dv = (callers
 // that would otherwise zero them first).
-static int mha_bwd_impl(aur_ctx* ctx, int overwrite, const float* q, const float* k, const float* v,
-                        uint32_t ld_qkv, const float* out, const float* d_out, uint32_t ld_out, const float* lse,
-                        float* dq, float* dk, float* dv, uint32_t ld_dqkv, float* ws, uint32_t b, uint32_t t,
-                        uint32_t n_head, uint32_t d_head) {
+// ws_tiled: the caller's ws holds tiled_ws_floats (the model's own arena).
+// Otherwise ws holds only what aur_mha_bwd_ws_bytes promises — at most the
+// reference's d_scores_scratch, n_head·t·t floats per sequence — and when the
+// tiled layout needs more than that (short or ragged t) D and the tiles go
+// to the context's workspace instead (refused while the stream is being
+// captured, since that workspace may be reallocated).
+static int mha_bwd_impl(aur_ctx* ctx, int overwrite, bool ws_tiled, const float* q, const float* k,
+                        const float* v, uint32_t ld_qkv, const float* out, const float* d_out, uint32_t ld_out,
+                        const float* lse, float* dq, float* dk, float* dv, uint32_t ld_dqkv, float* ws,
+                        uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head) {
   AUR_CHECK_CTX(ctx);
   if (int rc = check_common(ctx, b, t, n_head, d_head, ld_qkv, ld_out)) return rc;
   if (ld_dqkv < n_head * d_head || (ld_dqkv & 3))
@@ -876,6 +889,11 @@ static int mha_bwd_impl(aur_ctx* ctx, int overwrite, const float* q, const float
   if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(d_out) || !al16(dq) || !al16(dk) ||
       !al16(dv) || !al16(ws))
     return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: tensors must be 16-byte aligned");
+  const size_t tiled = tiled_ws_floats(b, t, n_head);
+  if (!ws_tiled && tiled > (size_t)b * n_head * t * t) {
+    if (int rc = aur::ensure_workspace(ctx, tiled * sizeof(float))) return rc;
+    ws = static_cast<float*>(ctx->ws);
+  }
   AttnArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = out; a.dO = d_out; a.lse = const_cast<float*>(lse);
   a.D = ws; a.dq = dq; a.dk = dk; a.dv = dv;
@@ -935,17 +953,15 @@ int aur_mha_fwd(aur_ctx* ctx, const float* q, const float* k, const float* v, fl
 }
 
 size_t aur_mha_bwd_ws_bytes(uint32_t b, uint32_t t, uint32_t n_head) {
-  const size_t nqt = (t + TQ - 1) / TQ;
-  return ws_d_floats(b, t, n_head) * sizeof(float) +
-         (size_t)b * n_head * (nqt * (nqt + 1) / 2) * TQ * TQ * sizeof(float);
+  return std::min(tiled_ws_floats(b, t, n_head), (size_t)b * n_head * t * t) * sizeof(float);
 }
 
 int aur_mha_bwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v, uint32_t ld_qkv,
                    const float* out, const float* d_out, uint32_t ld_out, const float* lse, float* dq,
                    float* dk, float* dv, uint32_t ld_dqkv, float* ws, uint32_t b, uint32_t t,
                    uint32_t n_head, uint32_t d_head) {
-  return mha_bwd_impl(ctx, 0, q, k, v, ld_qkv, out, d_out, ld_out, lse, dq, dk, dv, ld_dqkv, ws, b, t, n_head,
-                      d_head);
+  return mha_bwd_impl(ctx, 0, false, q, k, v, ld_qkv, out, d_out, ld_out, lse, dq, dk, dv, ld_dqkv, ws, b, t,
+                      n_head, d_head);
 }
 
 int aur_mha_bwd(aur_ctx* ctx, const float* q, const float* k, const float* v, const float* out,
@@ -963,8 +979,10 @@ int mha_bwd_store(aur_ctx* ctx, const float* q, const float* k, const float* v, 
                   const float* d_out, int ld_out, const float* lse, float* dq, float* dk, float* dv, int ld_dqkv,
                   float* ws, int b, int t, int n_head, int d_head) {
   AUR_CHECK_CTX(ctx);
-  return mha_bwd_impl(ctx, 1, q, k, v, (uint32_t)ld_qkv, out, d_out, (uint32_t)ld_out, lse, dq, dk, dv,
+  return mha_bwd_impl(ctx, 1, true, q, k, v, (uint32_t)ld_qkv, out, d_out, (uint32_t)ld_out, lse, dq, dk, dv,
                       (uint32_t)ld_dqkv, ws, (uint32_t)b, (uint32_t)t, (uint32_t)n_head, (uint32_t)d_head);
 }
+
+size_t mha_bwd_tiled_ws_floats(int b, int t, int n_head) { return tiled_ws_floats(b, t, n_head); }
 
 }  // namespace aur

@@ -417,10 +417,19 @@ void launch_seq(const KvArgs& a, int B, int t_max, hipStream_t st) {
   hipLaunchKernelGGL((kv_seq_kernel<DH, 2, 4, true>), dim3(a.H, B), dim3(64 * 4), 0, st, a, t_max);
 }
 
+// The chunked kernels write ceil(t/KC) records of PART floats per
+// (sequence, head) to the scratch, which must not need more than the
+// reference's scratch [n_head, max_len] per sequence (src/gpu/transformer.rs:
+// 2432).  They are used only when the records of a full-length history fit
+// in max_len floats; otherwise (max_len below PART, or just above a multiple
+// of KC) the scratch-free one-block-per-(sequence, head) kernel runs.
+bool chunks_fit(int max_len) { return (long)((max_len + KC - 1) / KC) * PART <= max_len; }
+
 int launch(aur_ctx* ctx, KvArgs& a, int B, int t_max, int d_head) {
   a.nch = (t_max + KC - 1) / KC;
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-  const bool seq = (long)B * a.H >= cus && std::getenv("AUR_KV_CHUNKED") == nullptr;
+  const bool seq = ((long)B * a.H >= cus && std::getenv("AUR_KV_CHUNKED") == nullptr) ||
+                   !chunks_fit(a.max_len);
 #define AUR_KV_CASE(DH) \
   case DH: seq ? launch_seq<DH>(a, B, t_max, ctx->stream) : launch_dh<DH>(a, B, ctx->stream); break
   switch (d_head) {
@@ -445,7 +454,8 @@ bool dh_ok(uint32_t d) { return d >= 8 && d <= 64 && d % 8 == 0; }
 extern "C" {
 
 size_t aur_mha_kv_ws_bytes(uint32_t b, uint32_t n_head, uint32_t max_len) {
-  return (size_t)b * n_head * ((max_len + KC - 1) / KC) * PART * sizeof(float);
+  const size_t nch = (max_len + KC - 1) / KC;
+  return chunks_fit((int)max_len) ? (size_t)b * n_head * nch * PART * sizeof(float) : 0;
 }
 
 int aur_mha_kv_step(aur_ctx* ctx, const float* q_new, const float* k_history, const float* v_history,

@@ -204,7 +204,7 @@ void DecoderTransformerGpu::init() {
                            H * M /*lse*/ + M * d /*xmid*/ + M * d /*ln2*/ + 2 * M + 2 * M * F;
   const size_t lnws = aur::layer_norm_backward_ws_floats((int)M, (int)d);
   // attention backward: rowdot + the causal dS tiles of max_batch sequences
-  const size_t attn_ws_floats = (aur_mha_bwd_ws_bytes(max_batch, (uint32_t)Tm, (uint32_t)H) + 3) / 4;
+  const size_t attn_ws_floats = aur::mha_bwd_tiled_ws_floats((int)max_batch, (int)Tm, (int)H);
   const size_t floats = L * per_layer + (L + 1) * M * d + M * d + 2 * M + M * V + M +
                         4 * M * d + M * F + 3 * M * d + lnws + attn_ws_floats + aur::grad_norm_ws_floats() + 16 +
                         (size_t)max_batch * d;

@@ -64,6 +64,9 @@ int embed_layer_norm(aur_ctx* ctx, const float* w_tok, const float* w_pos, const
 int gather_rows(aur_ctx* ctx, const float* src, int ld_src, int row_step, int row_off, float* dst,
                 int rows, int d);
 
+// Floats of the attention backward's tiled workspace (D + the causal dS
+// tiles) that mha_bwd_store's ws must hold (attention.hip).
+size_t mha_bwd_tiled_ws_floats(int b, int t, int n_head);
 // aur_mha_bwd_ex that STORES dq/dk/dv instead of accumulating (attention.hip).
 int mha_bwd_store(aur_ctx* ctx, const float* q, const float* k, const float* v, int ld_qkv, const float* out,
                   const float* d_out, int ld_out, const float* lse, float* dq, float* dk, float* dv, int ld_dqkv,

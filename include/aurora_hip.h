@@ -148,9 +148,12 @@ int aur_mha_fwd(aur_ctx* ctx, const float* q, const float* k, const float* v,
  * one writer, three passes (row dot D = Σ dO⊙O; dK/dV over query tiles,
  * which also stores the dS tiles of the causal lower triangle; dQ = dS·K
  * over those tiles).  `ws` is a caller-owned workspace of at least
- * aur_mha_bwd_ws_bytes(b, t, n_head) bytes: D [b,n_head,t] and the dS tiles,
- * ≈ b·n_head·t²/2 floats (it takes the slot of the reference's
- * d_scores_scratch [n_head,t,t] per sequence).
+ * aur_mha_bwd_ws_bytes(b, t, n_head) bytes, which never exceeds the
+ * reference's d_scores_scratch of n_head·t·t floats per sequence, and the
+ * call writes no more of it than that: D [b,n_head,t] and the dS tiles,
+ * ≈ b·n_head·t²/2 floats.  For short or ragged t, where the tiles need more
+ * than b·n_head·t² floats, they go to the context's own workspace instead
+ * (allocated on first need; AUR_EINVAL while the stream is being captured).
  * Replaces CausalMhaBackwardKernel::dispatch_into(ctx, enc, q, k, v, probs,
  * d_out, dq, dk, dv, d_scores_scratch, t, n_head, d_head)
  * (src/gpu/attention.rs:580-685). */
@@ -176,7 +179,10 @@ int aur_mha_bwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v,
 /* One new query per head against history rows [0, t_total):
  * q_new [n_head*d_head], k_history/v_history [max_len, n_head*d_head],
  * out [n_head*d_head].  `scratch` is caller-owned, at least
- * aur_mha_kv_ws_bytes(1, n_head, max_len) bytes.
+ * aur_mha_kv_ws_bytes(1, n_head, max_len) bytes, which never exceeds the
+ * reference's n_head·max_len floats (src/gpu/transformer.rs:2432): 68-float
+ * records per 128 keys where a full history's records fit in that, else 0
+ * bytes (the scratch-free one-block-per-head kernel runs).
  * Replaces MhaKvCacheKernel::dispatch_into(ctx, enc, q_new, k_history,
  * v_history, out, scratch, t_total, n_head, d_head, max_len)
  * (src/gpu/kv_cache.rs:421-465). */

@@ -57,10 +57,22 @@ def test_workspace_size_helpers():
     from aurora_amd import _lib
 
     lib = _lib.load()
-    # D [b, H, t] (256-byte padded) + the 64×64 dS tiles of the causal lower triangle
+    # D [b, H, t] (256-byte padded) + the 64×64 dS tiles of the causal lower
+    # triangle, never more than the reference's d_scores_scratch [H, t, t]
+    # per sequence (short or ragged t: the tiles then live in the context's
+    # own workspace and the caller's buffer is not written)
     assert lib.aur_mha_bwd_ws_bytes(16, 1024, 8) == (16 * 1024 * 8 + 16 * 8 * 136 * 4096) * 4
-    assert lib.aur_mha_bwd_ws_bytes(1, 65, 2) == (192 + 2 * 3 * 4096) * 4
-    assert lib.aur_mha_kv_ws_bytes(32, 16, 768) >= 32 * 16 * 6 * 66 * 4
+    assert lib.aur_mha_bwd_ws_bytes(1, 65, 2) == 2 * 65 * 65 * 4
+    assert lib.aur_mha_bwd_ws_bytes(1, 6, 2) == 72 * 4
+    for b, t, h in ((1, 6, 2), (1, 64, 2), (3, 65, 4), (2, 129, 8), (16, 1024, 8), (1, 1, 1)):
+        assert lib.aur_mha_bwd_ws_bytes(b, t, h) <= 4 * b * h * t * t
+    # 68-float chunk records per 128 keys, only where they fit the reference's
+    # scratch [n_head, max_len] per sequence; otherwise no scratch is used
+    assert lib.aur_mha_kv_ws_bytes(32, 16, 768) == 32 * 16 * 6 * 68 * 4
+    assert lib.aur_mha_kv_ws_bytes(1, 3, 256) == 3 * 2 * 68 * 4
+    assert lib.aur_mha_kv_ws_bytes(1, 2, 64) == 0 and lib.aur_mha_kv_ws_bytes(1, 2, 130) == 0
+    for b, h, m in ((1, 2, 64), (1, 2, 130), (4, 16, 200), (32, 16, 768), (1, 1, 1)):
+        assert lib.aur_mha_kv_ws_bytes(b, h, m) <= 4 * b * h * m
 
 
 def test_integration_rust_binding_covers_the_header():

@@ -315,3 +315,78 @@ def test_config2_zero_output_gradient_gives_zero_gradients(ctx):
     dq, dk, dv = _bwd(ctx, q, k, v, o, lse, np.zeros(n, np.float32), B, T, H, dh, init=init)
     for got, want in zip((dq, dk, dv), init):
         np.testing.assert_array_equal(got, want)
+
+
+# ------------------------------- the reference's own scratch allocations
+CANARY = 4096  # floats of guard on each side (16 KB: keeps the region 16-byte aligned)
+
+
+def _guarded(ctx, n):
+    """A device region of exactly n floats inside a larger allocation whose
+    two guard regions hold a known pattern: (buffer, view of the region)."""
+    from aurora_amd.gpu import GpuBuffer
+
+    host = np.full(CANARY + n + CANARY, 1234.5, np.float32)
+    host[CANARY:CANARY + n] = 0.0
+    buf = GpuBuffer.from_slice(ctx, host)
+    return buf, GpuBuffer(ctx, buf.ptr + 4 * CANARY, n)
+
+
+def _guards_intact(buf, n):
+    host = buf.download()
+    return bool(np.all(host[:CANARY] == 1234.5) and np.all(host[CANARY + n:] == 1234.5))
+
+
+@pytest.mark.parametrize("t,H,dh", [(6, 2, 8), (64, 2, 64), (65, 2, 16), (1, 1, 8)])
+def test_backward_within_reference_d_scores_allocation(ctx, t, H, dh):
+    """The reference allocates the backward's d_scores scratch as exactly
+    n_head·t·t floats (tests/gpu_parity.rs:292-297, src/gpu/transformer.rs:
+    314, 375): at its own parity case (t = 6, H = 2, d_head = 8: 72 floats)
+    and at short or ragged t, where the tiled dS layout needs more than that,
+    the call writes nothing outside those floats and matches the oracle."""
+    from aurora_amd.gpu import CausalMhaBackwardKernel, GpuBuffer
+
+    d = H * dh
+    rng = np.random.default_rng(0xB17D + t)
+    q, k, v, dy = (_n(rng, t * d) for _ in range(4))
+    o, lse = _fwd(ctx, q, k, v, 1, t, H, dh)
+    n_ws = H * t * t
+    assert CausalMhaBackwardKernel.workspace_len(t, H) <= n_ws
+    guard, ws = _guarded(ctx, n_ws)
+    bufs = [GpuBuffer.from_slice(ctx, x) for x in (q, k, v, o, lse, dy)]
+    grads = [GpuBuffer.zeros(ctx, t * d) for _ in range(3)]
+    CausalMhaBackwardKernel.new(ctx).dispatch_into(ctx, *bufs, *grads, ws, t, H, dh)
+    got = [g.download() for g in grads]
+    assert _guards_intact(guard, n_ws)
+    _, probs = oracle.mha_heads_forward(q, k, v, t, H, dh)
+    want = oracle.mha_heads_backward(q, k, v, probs, dy, t, H, dh)
+    for g, w in zip(got, want):
+        assert max_rel_err(g, w) < TOL_REF
+        assert fro_rel(g, w) < TOL_ATTN
+
+
+@pytest.mark.parametrize("max_len,t_total,H,dh", [(64, 64, 2, 64), (64, 17, 4, 32), (130, 130, 2, 64),
+                                                  (130, 100, 2, 16), (256, 200, 3, 64)])
+def test_kv_step_within_reference_scratch_allocation(ctx, max_len, t_total, H, dh):
+    """MhaKvCacheKernel's scratch is n_head·max_len floats in the reference
+    (src/gpu/transformer.rs:2432); the tiny preset decodes with max_len 64
+    (src/transformer/model.rs:108).  With exactly that allocation nothing is
+    written outside it, and the result matches the oracle (max_len 64 and 130
+    take the scratch-free kernel; 256 has room for the chunk records)."""
+    from aurora_amd.gpu import GpuBuffer, MhaKvCacheKernel
+
+    d = H * dh
+    rng = np.random.default_rng(max_len + t_total)
+    q_new = _n(rng, d)
+    kh, vh = _n(rng, max_len * d), _n(rng, max_len * d)
+    n_s = H * max_len
+    assert MhaKvCacheKernel.scratch_len(H, max_len) <= n_s
+    guard, scratch = _guarded(ctx, n_s)
+    bq, bk, bv = (GpuBuffer.from_slice(ctx, x) for x in (q_new, kh, vh))
+    out = GpuBuffer.zeros(ctx, d)
+    MhaKvCacheKernel.new(ctx).dispatch_into(ctx, bq, bk, bv, out, scratch, t_total, H, dh, max_len)
+    got = out.download()
+    assert _guards_intact(guard, n_s)
+    want = oracle.kv_attend(q_new, kh, vh, t_total, H, dh)
+    assert max_rel_err(got, want) < TOL_REF
+    assert fro_rel(got, want) < TOL_ATTN
