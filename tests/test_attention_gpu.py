@@ -204,8 +204,7 @@ def test_mha_kv_step_matches_cpu(ctx, t_total, H, dh):
     kh, vh = _n(rng, max_len * d), _n(rng, max_len * d)
     got = _kv_single(ctx, q_new, kh, vh, t_total, H, dh, max_len)
     want = oracle.kv_attend(q_new, kh, vh, t_total, H, dh)
-    assert max_rel_err(got, want) < TOL_REF
-    assert fro_rel(got, want) < TOL_ATTN
+    assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
 
 
 def test_kv_step_equals_last_row_of_full_forward(ctx):
@@ -360,9 +359,11 @@ def test_backward_within_reference_d_scores_allocation(ctx, t, H, dh):
     assert _guards_intact(guard, n_ws)
     _, probs = oracle.mha_heads_forward(q, k, v, t, H, dh)
     want = oracle.mha_heads_backward(q, k, v, probs, dy, t, H, dh)
-    for g, w in zip(got, want):
-        assert max_rel_err(g, w) < TOL_REF
-        assert fro_rel(g, w) < TOL_ATTN
+    g64 = causal_attention_grad_f64(*(x.reshape(1, t, H, dh).astype(np.float64) for x in (q, k, v, dy)))
+    for g, w, w64 in zip(got, want, g64):
+        # (row 0's dq is 0 in exact arithmetic: normalised metrics, as above)
+        assert fro_rel(g, w) < TOL_ATTN and max_norm_rel(g, w) < TOL_ATTN
+        assert fro_rel(g, w64) < TOL_ATTN and max_norm_rel(g, w64) < TOL_ATTN
 
 
 @pytest.mark.parametrize("max_len,t_total,H,dh", [(64, 64, 2, 64), (64, 17, 4, 32), (130, 130, 2, 64),
@@ -388,5 +389,4 @@ def test_kv_step_within_reference_scratch_allocation(ctx, max_len, t_total, H, d
     got = out.download()
     assert _guards_intact(guard, n_s)
     want = oracle.kv_attend(q_new, kh, vh, t_total, H, dh)
-    assert max_rel_err(got, want) < TOL_REF
-    assert fro_rel(got, want) < TOL_ATTN
+    assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
