@@ -13,6 +13,12 @@
   single tensors and of all parameters — a size-independent check of the
   whole backward (the reference's numerical-gradient test,
   tests/transformer_primitives.rs:40-93, scaled up).
+* The optimizers at config-3 width, against float64 restatements of the
+  reference's update rules applied to the gradients the GPU computed:
+  the Muon hybrid (one layer at V 8192, d 1024, d_ff 4096; two steps so
+  that the momentum takes part; the Newton–Schulz products on 1024 × 1024
+  and 1024 × 4096 matrices) and clip + AdamW on the full 12-layer model
+  (1.6·10⁸ parameters: the device's two-level norm against a float64 norm).
 * Config 4 in full: 32 prompts of 512, all 256 greedy decode steps (KV to
   768): every step's logits against one full forward over the generated
   sequences, greedy tokens against that forward's argmax position by
@@ -122,6 +128,108 @@ def test_config3_full_model_directional_derivatives(ctx):
         assert rel < 1e-2, (name, layer, gn, fd)
     assert abs(mean_loss() - loss) < 1e-6 * loss  # parameters restored
     print(f"[c3 ddir] worst relative error {worst:.2e}", flush=True)
+    m.destroy()
+
+
+def _decayed(name):
+    """model.rs:926-1009: decoupled decay on w_tok and the block matrices."""
+    return name == "w_tok" or name in OM.DECAY_KEYS
+
+
+def _adamw64(p, g, m1, m2, step, lr, wd, decay, b1=0.9, b2=0.95, eps=1e-8):
+    """optimizer.rs:58-90 in float64; updates m1 / m2 in place, returns p'."""
+    m1 *= b1
+    m1 += (1 - b1) * g
+    m2 *= b2
+    m2 += (1 - b2) * g * g
+    upd = lr * (m1 / (1 - b1 ** step)) / (np.sqrt(m2 / (1 - b2 ** step)) + eps)
+    return p - upd - (lr * wd * p if decay else 0.0)
+
+
+def _ns5_64(u, rows, cols, steps=5):
+    """optimizer.rs:147-252 in float64: Frobenius bound, wide orientation,
+    X' = aX + (bA + cA²)X with A = XXᵀ, back to rows × cols."""
+    x = u.reshape(rows, cols) / (np.sqrt(np.sum(u * u)) + 1e-7)
+    if rows > cols:
+        x = x.T
+    for _ in range(steps):
+        a = x @ x.T
+        x = 3.4445 * x + (-4.7750 * a + 2.0315 * (a @ a)) @ x
+    return (x.T if rows > cols else x).reshape(-1)
+
+
+def test_config3_width_muon_hybrid_matches_float64(ctx):
+    """Two step_muon_hybrid calls (after clip_grads_adamw_subset at 1.0) on
+    one config-3-width layer, from the gradients of one B1 T1024 step,
+    against model.rs:1023-1107 / optimizer.rs:94-305 in float64: the subset
+    norm to 1e-5, every tensor's update to 1e-3 and the parameters to 1e-5
+    (the config-0 gates)."""
+    cfg = OM.Config(vocab=8192, d_model=1024, n_layer=1, n_head=16, d_ff=4096, seq_len_max=1024)
+    d, F = cfg.d_model, cfg.d_ff
+    P = OM.init_params(cfg, 2)
+    tok, tgt = _tokens(cfg.vocab, 1, 1024, 9)
+    m = _model(ctx, cfg, 1, P)
+    m.zero_grad()
+    m.train_step_batch(tok, tgt)
+    G = m.read_tensors(grad=True)
+    P0 = m.read_tensors(grad=False)
+    n_gpu = m.clip_grads_adamw_subset(1.0)
+    flat = lambda T: [(n, l, np.asarray(a, np.float64).ravel()) for n, l, a in OM.tensors(T)]  # noqa: E731
+    g64, p64 = flat(G), flat(P0)
+    sub = {"w_tok", "w_pos", "ln1_g", "ln1_b", "ln2_g", "ln2_b", "lnf_g", "lnf_b"}  # model.rs:518-560
+    n64 = np.sqrt(sum(np.sum(g * g) for n, _, g in g64 if n in sub))
+    assert abs(n_gpu - n64) < 1e-5 * n64, (n_gpu, n64)
+    f = min(1.0, 1.0 / n64)
+    shapes = {"w_q": (d, d), "w_k": (d, d), "w_v": (d, d), "w_o": (d, d), "w_fc": (d, F), "w_proj": (F, d)}
+    state = [(np.zeros_like(g), np.zeros_like(g)) for _, _, g in g64]
+    cur = [p.copy() for _, _, p in p64]
+    for step in (1, 2):
+        m.step_muon_hybrid(muon_lr=0.02, momentum=0.95, nesterov=True, muon_wd=0.01, ns_steps=5, lr=3e-4,
+                           weight_decay=0.1)
+        prev = [c.copy() for c in cur]
+        for i, (name, _, g) in enumerate(g64):
+            if name in sub:
+                cur[i] = _adamw64(cur[i], g * f, *state[i], step, 3e-4, 0.1, name == "w_tok")
+            else:
+                mom = state[i][0]
+                mom *= 0.95
+                mom += g
+                rows, cols = shapes[name]
+                upd = _ns5_64(g + 0.95 * mom, rows, cols) * np.sqrt(max(rows, cols) / min(rows, cols))
+                cur[i] = cur[i] - 0.02 * upd - 0.02 * 0.01 * cur[i]
+        got = flat(m.read_tensors(grad=False))
+        for (name, l, a), c, c0 in zip(got, cur, prev):
+            assert fro_rel(a - c0, c - c0) < 1e-3, (step, name, l, fro_rel(a - c0, c - c0))
+            assert fro_rel(a, c) < 1e-5, (step, name, l)
+    m.destroy()
+
+
+def test_config3_full_model_clip_adamw_matches_float64(ctx):
+    """clip_grads(1.0) + step_adamw on the full config-3 model (12 layers,
+    1.6·10⁸ parameters) from one B1 T1024 step: the device's two-level L2
+    norm against a float64 norm of the downloaded gradients (1e-5 relative)
+    and every tensor after the step against optimizer.rs:58-90 in float64
+    with the reference's decay groups."""
+    cfg = C3
+    P = OM.init_params(cfg, 2)
+    tok, tgt = _tokens(cfg.vocab, 1, 1024, 10)
+    m = _model(ctx, cfg, 1, P)
+    del P
+    m.zero_grad()
+    m.train_step_batch(tok, tgt)
+    G = m.read_tensors(grad=True)
+    P0 = m.read_tensors(grad=False)
+    n64 = np.sqrt(sum(np.sum(np.asarray(a, np.float64) ** 2) for _, _, a in OM.tensors(G)))
+    n_gpu = m.clip_grads(1.0)
+    assert abs(n_gpu - n64) < 1e-5 * n64, (n_gpu, n64)
+    m.step_adamw(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    f = min(1.0, 1.0 / n64)
+    got = m.read_tensors(grad=False)
+    for (name, l, a), (_, _, g), (_, _, p) in zip(OM.tensors(got), OM.tensors(G), OM.tensors(P0)):
+        g64, p64 = np.asarray(g, np.float64).ravel() * f, np.asarray(p, np.float64).ravel()
+        want = _adamw64(p64, g64, np.zeros_like(g64), np.zeros_like(g64), 1, 3e-4, 0.1, _decayed(name))
+        assert fro_rel(np.asarray(a, np.float64) - p64, want - p64) < 1e-3, (name, l)
+        assert fro_rel(a, want) < 1e-6, (name, l)
     m.destroy()
 
 
