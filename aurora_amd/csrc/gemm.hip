@@ -976,7 +976,7 @@ constexpr int kBK = 32;
 // MI355X to every forced configuration (6 tiles × split-K 1…16) of 50
 // shapes — the config-1 and config-3 GEMMs of all three forms at M = 8192 /
 // 16384 and at one GPU's 8-way data-parallel share, M = 1024 / 2048 — timed
-// by aurora_amd/tune_gemm.py: tile efficiency 1.00 / 0.95 / 0.90 / 0.70 /
+// by `bench.py --only planner`: tile efficiency 1.00 / 0.95 / 0.90 / 0.70 /
 // 0.55 (128×128 / 128×64 / 64×64 / 64×32 / 32×32), single-block factor 0.95
 // / 0.95 / 0.85 / 0.7 / 0.7 (the software-pipelined main loop keeps one
 // wave per SIMD nearly as busy as two), 3 TB/s for the reduction and 2 µs

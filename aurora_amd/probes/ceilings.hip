@@ -4,7 +4,11 @@
 //   * a streaming read of a buffer far larger than the caches (the best of
 //     a few load depths and grid sizes),
 //   * an empty kernel replayed from a HIP graph (the fixed cost every
-//     launch of the captured decode step pays).
+//     launch of the captured decode step pays),
+//   * reads of a few MB replayed from a HIP graph, each launch reading its
+//     own slice of a buffer larger than the last-level cache (cold: what a
+//     decode-step kernel streaming one weight matrix once could cost) or all
+//     the same slice (warm).
 // A measurement aid built next to the library (libaurora_ceilings.so), not
 // part of its C ABI.  All launches go to the caller's stream.
 #include <hip/hip_runtime.h>
@@ -119,6 +123,33 @@ int ceil_graph_create(void* stream, int n, void** exec) {
   hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
   if (e != hipSuccess) return (int)e;
   for (int i = 0; i < n; ++i) hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, st);
+  hipGraph_t g = nullptr;
+  e = hipStreamEndCapture(st, &g);
+  if (e != hipSuccess) return (int)e;
+  hipGraphExec_t ex = nullptr;
+  e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return (int)e;
+  *exec = ex;
+  return 0;
+}
+
+// Captures `n` dependent reads of `slice_bytes` each (a multiple of 16) on
+// `stream` into a graph: launch i reads src + i·slice_bytes when cold != 0,
+// else src every time.  blocks / mode as ceil_stream_read; the caller owns
+// n·slice_bytes (cold) or slice_bytes (warm) at src.
+int ceil_graph_reads_create(void* stream, const void* src, size_t slice_bytes, int n, int blocks, int mode,
+                            int cold, float* sink, void** exec) {
+  if (n <= 0 || !exec || blocks <= 0 || !src || !sink || slice_bytes % 16 != 0 || mode < 0 || mode > 2)
+    return (int)hipErrorInvalidValue;
+  *exec = nullptr;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return (int)e;
+  for (int i = 0; i < n; ++i) {
+    const char* p = static_cast<const char*>(src) + (cold ? (size_t)i * slice_bytes : 0);
+    (void)ceil_stream_read(stream, p, slice_bytes, blocks, mode, sink);
+  }
   hipGraph_t g = nullptr;
   e = hipStreamEndCapture(st, &g);
   if (e != hipSuccess) return (int)e;

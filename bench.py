@@ -33,8 +33,8 @@ PEAK_HBM = 8000.0       # GB/s
 CLOCK_RAMP_S = 0.25     # untimed sustained work before a timed GEMM region
 COPY_MIB = 256          # calibration copy of the --only traffic leg
 # HBM bytes per head-GEMM launch from the two counter passes of
-# profiles/gemm_head_nt_8192x8192x512_traffic.md: FETCH_SIZE 108751.9 KiB × 2.000
-# + WRITE_SIZE 262156.3 KiB × 1.000 (factors from the 256 MiB copy).
+# profiles/gemm_head_nt_8192x8192x512_traffic.md: FETCH_SIZE 156261.9 KiB × 2.000
+# + WRITE_SIZE 262144.4 KiB × 1.000 (factors from the 256 MiB copy).
 HEAD_TRAFFIC_BYTES = (156261.9 * 2.000 + 262144.4 * 1.000) * 1024
 SWEEP_KN = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
 M = 8192
@@ -204,6 +204,8 @@ def bench_ceilings(ctx, cus: int) -> dict:
     lib.ceil_mfma_f32_32x32.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
     lib.ceil_stream_read.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_void_p]
     lib.ceil_graph_create.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_void_p)]
+    lib.ceil_graph_reads_create.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int,
+                                            C.c_int, C.c_void_p, C.POINTER(C.c_void_p)]
     lib.ceil_graph_launch.argtypes = [C.c_void_p, C.c_void_p]
     lib.ceil_graph_destroy.argtypes = [C.c_void_p]
     stream = _lib.load().aur_stream(ctx.ptr)
@@ -249,16 +251,115 @@ def bench_ceilings(ctx, cus: int) -> dict:
         ok(lib.ceil_graph_launch(stream, ex), "ceil_graph_launch")
     ms_g = time_region(ctx, lambda: ok(lib.ceil_graph_launch(stream, ex), "ceil_graph_launch"), 20)
     ok(lib.ceil_graph_destroy(ex), "ceil_graph_destroy")
+
+    # Reads the size of one decode weight matrix (W_o 4 MB, QKV 12.6 MB,
+    # fc / W_proj 16.8 MB), replayed from a graph as the decode step is:
+    # cold = every launch reads its own slice of 1 GiB (beyond the 256 MB
+    # last-level cache), warm = every launch reads the same slice.
+    big = GpuBuffer.zeros(ctx, (1 << 30) // 4)
+    small_reads = {}
+    for mib in (4, 8, 16):
+        slice_b = mib << 20
+        n = (1 << 30) // slice_b
+        for cold in (1, 0):
+            best_us, best_cfg = None, None
+            for blocks, mode in ((cus, 1), (cus, 2), (2 * cus, 1), (2 * cus, 2)):
+                ok(lib.ceil_graph_reads_create(stream, big.ptr, slice_b, n, blocks, mode, cold, sink.ptr,
+                                               C.byref(ex)), "ceil_graph_reads_create")
+                for _ in range(2):
+                    ok(lib.ceil_graph_launch(stream, ex), "ceil_graph_launch")
+                us = time_region(ctx, lambda: ok(lib.ceil_graph_launch(stream, ex), "ceil_graph_launch"), 5) \
+                    * 1e3 / n
+                ok(lib.ceil_graph_destroy(ex), "ceil_graph_destroy")
+                if best_us is None or us < best_us:
+                    best_us, best_cfg = us, f"{blocks // cus} blocks/CU, {'NT ' if mode == 2 else ''}8 loads"
+            small_reads[f"{mib} MiB {'cold' if cold else 'warm'}"] = {
+                "us": round(best_us, 2), "gbs": round(slice_b / (best_us * 1e-6) / 1e9, 1), "best": best_cfg}
+    big.free()
     sink.free()
     out = {"mfma_fp32_tflops": round(mfma_tf, 1), "mfma_fp32_frac_of_peak": round(mfma_tf / PEAK_FP32_MFMA, 3),
            "mfma_fp32_32x32x2_tflops": round(mfma32_tf, 1),
            "hbm_read_gbs": round(read_gbs, 1), "hbm_read_frac_of_peak": round(read_gbs / PEAK_HBM, 3),
            "hbm_read_best": best, "hbm_read_all_gbs": {k: round(v, 1) for k, v in reads.items()},
            "graph_empty_kernel_us": round(ms_g * 1e3 / n_launch, 2),
+           "graph_reads": small_reads,
            "probes": "register-operand fp32 MFMA (16x16x4, and 32x32x2), 2 GiB streaming read, "
-                     "empty kernel in a HIP graph"}
+                     "empty kernel in a HIP graph, 4-16 MiB reads replayed from a HIP graph (cold / warm)"}
     log(f"[bench] ceilings {out}")
     return out
+
+
+PLANNER_TILES = ["256x128", "128x128", "128x64", "64x64", "64x32", "32x32"]
+PLANNER_SPLITS = [1, 2, 4, 8, 16]
+
+
+def planner_shapes(which: str) -> list[tuple[str, int, int, int]]:
+    """(form, M, N, K) of the planner sweep: form nt (A@Bᵀ), nn (A@B) or acc
+    (weight-gradient accumulate: M = d_out, N = d_in, K = t) — the config-1
+    and config-3 GEMMs at M = 8192 / 16384 and at one GPU's 8-way
+    data-parallel share, M = 1024 / 2048."""
+    c3_nk = [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096), (8192, 1024)]  # forward N, K
+    c3_nn = [(1024, 3072), (1024, 1024), (1024, 4096), (4096, 1024), (1024, 8192)]  # dX N, K
+    out = []
+    for m in ([8192] if which in ("c1", "all") else []) + ([1024] if which in ("dp8", "all") else []):
+        for k, n in SWEEP_KN:
+            out += [("nn", m, n, k), ("nt", m, n, k)]
+        out += [("nt", m, 8192, 512), ("acc", 2048, 512, m)]
+    for m in ([16384] if which in ("c3", "all") else []) + ([2048] if which in ("dp8", "all") else []):
+        out += [("nt", m, n, k) for n, k in c3_nk]
+        out += [("nn", m, n, k) for n, k in c3_nn]
+        out += [("acc", o, i, m) for o, i in c3_nk]
+    return out
+
+
+def bench_planner(ctx, steps: int, which: str) -> None:
+    """The GEMM launch-plan sweep the planner constants in gemm.hip
+    (choose_plan) are fitted to: every forced tile / split-K configuration
+    (AUR_GEMM_CFG="BMxBN:splits", which the library reads on every call) of
+    each shape, next to the planner's own pick.  One line per (form, shape)
+    on stdout: "form MxNxK: auto=<TFLOP/s> cfg=<TFLOP/s> ..."; inputs are
+    seeded U(-1,1) fp32 in HBM."""
+    from aurora_amd.gpu import GpuBuffer
+
+    rng = np.random.default_rng(0)
+    shapes = planner_shapes(which)
+    big = max(max(m * k, n * k, m * n) for _, m, n, k in shapes)
+    a, b, c = (GpuBuffer.from_slice(ctx, rng.uniform(-1, 1, big).astype(np.float32)) for _ in range(3))
+
+    def launch(form, m, n, k):
+        if form == "acc":  # dest[m,n] += Σ_t d_y[t,m]·x[t,n]
+            ctx.call("aur_outer_accum", a.ptr, b.ptr, c.ptr, m, n, k)
+        else:
+            ctx.call("aur_gemm_" + form, a.ptr, b.ptr, c.ptr, m, n, k)
+
+    def tflops(cfg, form, m, n, k):
+        if cfg is None:
+            os.environ.pop("AUR_GEMM_CFG", None)
+        else:
+            os.environ["AUR_GEMM_CFG"] = cfg
+        for _ in range(5):
+            launch(form, m, n, k)
+        ms = time_region(ctx, lambda: launch(form, m, n, k), steps)
+        return 2.0 * m * n * k / (ms * 1e-3) / 1e12
+
+    ramp_end = time.perf_counter() + CLOCK_RAMP_S
+    while time.perf_counter() < ramp_end:
+        for _ in range(10):
+            launch("nt", 8192, 8192, 512)
+        ctx.sync()
+    for form, m, n, k in shapes:
+        res = [f"auto={tflops(None, form, m, n, k):.1f}"]
+        for t in PLANNER_TILES:
+            if t == "256x128" and form == "acc":
+                continue  # the 256-row tile needs A k-contiguous (planner: allow_wide)
+            for sp in PLANNER_SPLITS:
+                if sp > 1 and k // sp < 64:
+                    break
+                res.append(f"{t}:{sp}={tflops(f'{t}:{sp}', form, m, n, k):.1f}")
+        print(f"{form} {m}x{n}x{k}: " + " ".join(res), flush=True)
+    os.environ.pop("AUR_GEMM_CFG", None)
+    for x in (a, b, c):
+        x.free()
 
 
 def bench_vendor(steps: int) -> None:
@@ -611,10 +712,12 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", choices=["head", "sweep", "train", "decode", "attention", "traffic", "shapes",
-                                       "ceilings", "vendor"],
+                                       "ceilings", "vendor", "planner"],
                     default=None,
                     help="profile helper: time only this part and skip the CPU baseline")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--planner-set", choices=["all", "c1", "c3", "dp8"], default="all",
+                    help="shapes of --only planner")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--cpu-train", choices=["full", "sample"], default="full",
                     help="full: time a whole config-3 CPU step (about a minute on 16 cores); "
@@ -675,6 +778,9 @@ def main() -> int:
         return 0
     if args.only == "shapes":
         bench_c3_and_shards(ctx, args.steps)
+        return 0
+    if args.only == "planner":
+        bench_planner(ctx, args.steps, args.planner_set)
         return 0
     if args.only == "ceilings":
         bench_ceilings(ctx, cus)
