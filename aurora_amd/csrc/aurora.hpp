@@ -379,6 +379,7 @@ class KvCacheGpu {
   float *x_ = nullptr, *ln_ = nullptr, *qkv_ = nullptr, *attn_ = nullptr, *xmid_ = nullptr;
   float *hpre_ = nullptr, *hpost_ = nullptr, *logits_ = nullptr, *scratch_ = nullptr;
   float* part_ = nullptr;  // K-range partial products of the W_o / W_proj decode GEMMs
+  float* pf_sink_ = nullptr;  // the L2 prefetch blocks' never-written sink
   size_t part_floats_ = 0;
   int qkv_parts = 1;  // K ranges of the decode QKV projection held in qkv_
   int o_parts = 1, p_parts = 1;  // K ranges of the W_o / W_proj products in part_

@@ -119,7 +119,34 @@ struct KvArgs {
   // the value is the sum of nparts (≤ 8) rows pstride floats apart, in order.
   int nparts;
   size_t pstride;
+  // Blocks with blockIdx.y >= nseq only prefetch (kv_seq_kernel).
+  int nseq;
+  aur::L2Prefetch pf;
 };
+
+// Prefetch block `slot` of XCD `xcd` loads its share of the row groups
+// x ≡ xcd (mod 8) of every matrix of the plan, 16 bytes per lane, with
+// ordinary (L2-allocating) loads; the values are only summed so the loads
+// are kept.
+__device__ void l2_prefetch(const aur::L2Prefetch& pf, int xcd, int slot) {
+  float acc = 0.f;
+  for (int m = 0; m < pf.nmat; ++m) {
+    const int G = pf.group[m];
+    const size_t gf4 = (size_t)G * pf.row_floats[m] / 4;  // float4 per row group
+    const int ngroups = pf.rows[m] / G;
+    const int mine = ngroups > xcd ? (ngroups - xcd + 7) / 8 : 0;  // groups of this XCD
+    const size_t total = (size_t)mine * gf4;
+    const size_t per = (total + pf.blocks_per_xcd - 1) / pf.blocks_per_xcd;
+    const size_t b0 = (size_t)slot * per, b1 = b0 + per < total ? b0 + per : total;
+    const floatx4* base = reinterpret_cast<const floatx4*>(pf.ptr[m]);
+    for (size_t f = b0 + threadIdx.x; f < b1; f += blockDim.x) {
+      const size_t t = f / gf4, within = f - t * gf4;
+      const floatx4 v = base[(xcd + 8 * t) * gf4 + within];
+      acc += v[0];
+    }
+  }
+  if (acc == 1.2345678e-38f) *pf.sink = acc;
+}
 
 // Σ_z p[z·stride] for z < np (≤ 8), ascending; the loads are all issued
 // before the adds (clamped index, branch-free).
@@ -266,6 +293,11 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
   __shared__ float wm[SW], wl[SW];
   __shared__ __attribute__((aligned(16))) float wo[SW][DH];
   __shared__ __attribute__((aligned(16))) float qkn[3][DH];  // q (scaled), new k, new v of this head
+  if ((int)blockIdx.y >= a.nseq) {  // appended prefetch blocks (a.nseq·H is a multiple of 8)
+    const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+    l2_prefetch(a.pf, lin % 8, (lin - a.nseq * (int)gridDim.x) / 8);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane / LPK, part = lane % LPK;
   const bool live = part < NP;          // a lane of the group past the row is idle
@@ -414,7 +446,9 @@ void launch_seq(const KvArgs& a, int B, int t_max, hipStream_t st) {
   // best shape without non-temporal loads 0.864.  A plain 2 GiB read
   // behaves alike: fastest with two 4-wave blocks per CU and non-temporal
   // loads (6.5 TB/s; 5.0-5.9 TB/s with more waves per CU or cached loads).
-  hipLaunchKernelGGL((kv_seq_kernel<DH, 2, 4, true>), dim3(a.H, B), dim3(64 * 4), 0, st, a, t_max);
+  // Prefetch blocks: whole rows of H blocks, 8·blocks_per_xcd of them.
+  const int extra = a.pf.nmat > 0 ? (8 * a.pf.blocks_per_xcd + a.H - 1) / a.H : 0;
+  hipLaunchKernelGGL((kv_seq_kernel<DH, 2, 4, true>), dim3(a.H, B + extra), dim3(64 * 4), 0, st, a, t_max);
 }
 
 // The chunked kernels write ceil(t/KC) records of PART floats per
@@ -449,6 +483,8 @@ int launch(aur_ctx* ctx, KvArgs& a, int B, int t_max, int d_head) {
 
 bool dh_ok(uint32_t d) { return d >= 8 && d <= 64 && d % 8 == 0; }
 
+bool aligned16_kv(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 }  // namespace
 
 extern "C" {
@@ -471,6 +507,7 @@ int aur_mha_kv_step(aur_ctx* ctx, const float* q_new, const float* k_history, co
   KvArgs a{};
   a.q = q_new; a.kh = k_history; a.vh = v_history; a.out = out; a.ws = scratch;
   a.t_dev = nullptr; a.t_scalar = (int)t_total;
+  a.nseq = 1;
   a.ld = (int)(n_head * d_head); a.ld_q = a.ld; a.max_len = (int)max_len; a.H = (int)n_head;
   a.scale = 1.0f / sqrtf((float)d_head);
   return launch(ctx, a, 1, (int)t_total, (int)d_head);
@@ -492,7 +529,7 @@ namespace aur {
 int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_history,
                    const float* v_history, float* out, float* scratch, const int32_t* t_total, int t_max,
                    int b, int n_head, int d_head, int max_len, const float* k_new, const float* v_new,
-                   int nparts, size_t part_stride) {
+                   int nparts, size_t part_stride, const L2Prefetch* prefetch) {
   if (!dh_ok((uint32_t)d_head))
     return set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%d, supports multiples of 8 up to 64", d_head);
   if (b <= 0 || n_head <= 0 || t_max <= 0 || t_max > max_len || ld_q < n_head * d_head || (ld_q & 3))
@@ -509,6 +546,19 @@ int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_histor
   a.scale = 1.0f / sqrtf((float)d_head);
   a.knew = k_new; a.vnew = v_new;
   a.nparts = nparts; a.pstride = part_stride;
+  a.nseq = b;
+  if (prefetch && prefetch->nmat > 0) {
+    // Only the one-block-per-(sequence, head) kernel carries prefetch blocks
+    // (the chunked kernels ignore the plan), and their slot arithmetic needs
+    // the attention blocks to fill whole rounds of the 8 XCDs.
+    if ((b * n_head) % 8 == 0 && prefetch->blocks_per_xcd > 0 && prefetch->nmat <= 3 && prefetch->sink) {
+      bool ok = true;
+      for (int m = 0; m < prefetch->nmat; ++m)
+        ok = ok && prefetch->ptr[m] && prefetch->group[m] > 0 && prefetch->rows[m] % prefetch->group[m] == 0 &&
+             prefetch->row_floats[m] % 4 == 0 && aligned16_kv(prefetch->ptr[m]);
+      if (ok) a.pf = *prefetch;
+    }
+  }
   return launch(ctx, a, b, t_max, d_head);
 }
 

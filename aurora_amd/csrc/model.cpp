@@ -730,7 +730,7 @@ KvCacheGpu::KvCacheGpu(DecoderTransformerGpu& model, uint32_t batch_, uint32_t m
   part_floats_ = (size_t)std::max(o_parts, p_parts) * B * d;
   // x, ln, qkv (3 per part), attn, xmid rows of d per sequence
   const size_t floats =
-      2 * hist + B * (d * (4 + 3 * (size_t)qkv_parts) + 2 * F + V) + scratch + part_floats_;
+      2 * hist + B * (d * (4 + 3 * (size_t)qkv_parts) + 2 * F + V) + scratch + part_floats_ + 64;
   bytes_ = floats * 4 + 3 * B * 4 + 40 * 256;
   ck(ctx_, aur_malloc(ctx_, bytes_, &mem_), "KvCacheGpu alloc");
   Carver cv{static_cast<char*>(mem_)};
@@ -746,6 +746,7 @@ KvCacheGpu::KvCacheGpu(DecoderTransformerGpu& model, uint32_t batch_, uint32_t m
   logits_ = cv.take<float>(B * V);
   scratch_ = cv.take<float>(scratch);
   part_ = cv.take<float>(part_floats_);
+  pf_sink_ = cv.take<float>(64);
   pos_ = cv.take<int32_t>(B);
   lens_ = cv.take<int32_t>(B);
   tok_ = cv.take<uint32_t>(B);
@@ -911,10 +912,32 @@ void DecoderTransformerGpu::encode_decode_step(KvCacheGpu& cache) {
       ck(ctx_, aur::gemm(ctx_, true, true, cache.ln_, d, Y.w_qkv, d, cache.qkv_, 3 * d, B, 3 * d, d, store),
          "qkv");
     // attention of the new query over history + the new row, which the
-    // kernel also appends to the history (kv_cache.rs:169-179)
+    // kernel also appends to the history (kv_cache.rs:169-179); its extra
+    // blocks pull the following GEMMs' weights into the L2 of the XCDs whose
+    // blocks will read them
+    aur::L2Prefetch pf;
+    if (const char* env = std::getenv("AUR_DEC_PREFETCH")) {
+      const char* nb = std::getenv("AUR_DEC_PF_BLOCKS");
+      pf.blocks_per_xcd = nb ? std::atoi(nb) : 32;
+      pf.sink = cache.pf_sink_;
+      auto add = [&](const float* w, int rows, int row_floats, int group) {
+        if (pf.nmat < 3 && (rows / group) % 8 == 0) {
+          pf.ptr[pf.nmat] = w;
+          pf.rows[pf.nmat] = rows;
+          pf.row_floats[pf.nmat] = row_floats;
+          pf.group[pf.nmat] = group;
+          ++pf.nmat;
+        }
+      };
+      for (const char* c = env; *c; ++c) {
+        if (*c == 'o') add(Y.w_o, d, d, split ? 64 : 16);  // stream_partials: 64 columns per block
+        if (*c == 'f') add(Y.w_fc, F, d, 16);              // skinny: 16 columns per block
+        if (*c == 'p') add(Y.w_proj, d, F, split ? 64 : 16);
+      }
+    }
     ck(ctx_, aur::mha_kv_batched(ctx_, cache.qkv_, 3 * d, cache.k_history(l), cache.v_history(l), cache.attn_,
                                  cache.scratch_, cache.lens_, t_max, B, H, dh, (int)cache.max_len,
-                                 cache.qkv_ + d, cache.qkv_ + 2 * d, cache.qkv_parts, (size_t)B * 3 * d),
+                                 cache.qkv_ + d, cache.qkv_ + 2 * d, cache.qkv_parts, (size_t)B * 3 * d, &pf),
        "mha_kv");
     if (split) {
       ck(ctx_, aur::gemm_nt_partials(ctx_, cache.attn_, d, Y.w_o, d, cache.part_, B, d, d, s_o), "w_o");

@@ -77,9 +77,27 @@ int mha_bwd_store(aur_ctx* ctx, const float* q, const float* k, const float* v, 
 // them and appended to the history by the kernel.  nparts > 1: q, k_new and
 // v_new are each the sum of nparts (≤ 8) K-range partial rows part_stride
 // floats apart (the QKV projection's partials), summed in order.
+// Weights of the GEMMs that follow the decode attention, to be pulled into
+// the L2 of the XCD whose blocks will read them while the attention streams
+// the K/V history (which it loads non-temporally, past L2).  Matrix m is
+// [rows[m], row_floats[m]] row-major; its consumer runs column blocks of
+// group[m] weight rows, block x on XCD x % 8 (the consumer's gridDim.x is a
+// multiple of 8 and workgroups go to the XCDs round-robin), so XCD j gets
+// the row groups x ≡ j (mod 8).
+struct L2Prefetch {
+  int nmat = 0;
+  const float* ptr[3] = {nullptr, nullptr, nullptr};
+  int rows[3] = {0, 0, 0};
+  int row_floats[3] = {0, 0, 0};
+  int group[3] = {0, 0, 0};
+  int blocks_per_xcd = 0;  // prefetch blocks per XCD appended to the launch
+  float* sink = nullptr;   // 1 float, written only if the loaded values sum to a sentinel
+};
+
 int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_history,
                    const float* v_history, float* out, float* scratch, const int32_t* t_total, int t_max,
                    int b, int n_head, int d_head, int max_len, const float* k_new = nullptr,
-                   const float* v_new = nullptr, int nparts = 1, size_t part_stride = 0);
+                   const float* v_new = nullptr, int nparts = 1, size_t part_stride = 0,
+                   const L2Prefetch* prefetch = nullptr);
 
 }  // namespace aur

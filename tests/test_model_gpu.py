@@ -473,6 +473,33 @@ def test_greedy_kv_decode_token_identical_to_full_forward(ctx):
     m.destroy()
 
 
+def test_decode_l2_prefetch_leaves_results_unchanged(ctx, monkeypatch):
+    """AUR_DEC_PREFETCH (read when the decode step is captured) appends
+    blocks to the KV attention that pull the following GEMMs' weights into
+    L2; they only load, so every logit of every step is bit-identical."""
+    cfg = OM.Config(vocab=256, d_model=512, n_layer=2, n_head=16, d_ff=1024, seq_len_max=64)
+    P = OM.init_params(cfg, 17)
+    B = 32  # B·H = 512 pairs: the one-block-per-(sequence, head) kernel
+    prompts = np.random.default_rng(17).integers(0, cfg.vocab, (B, 24)).astype(np.uint32)
+    m = _gpu_model(ctx, cfg, B, P)
+
+    def run():
+        cache = m.kv_cache(B, cfg.seq_len_max)
+        out = [m.prefill_kv(cache, prompts)]
+        for _ in range(8):
+            out.append(m.generate_step_kv(cache)[0])
+        cache.destroy()
+        return out
+
+    plain = run()
+    monkeypatch.setenv("AUR_DEC_PREFETCH", "ofp")
+    for blocks in ("32", "7"):
+        monkeypatch.setenv("AUR_DEC_PF_BLOCKS", blocks)
+        for a, b in zip(plain, run()):
+            np.testing.assert_array_equal(a, b)
+    m.destroy()
+
+
 def test_failed_model_create_frees_its_memory(ctx):
     """A model whose activation arena cannot be allocated (max_batch 4096 at
     the config-3 width asks for about a terabyte) fails with the allocator's
