@@ -1,5 +1,5 @@
 // Causal multi-head attention on gfx950 fp32 matrix cores, d_head any multiple
-// of 8 up to 64.
+// of 8 up to 64 (any other d_head up to 64 through zero-padded heads).
 //
 // Reference semantics (src/attention.rs:396-550, src/gpu/attention.rs:21-331):
 //   S = Q_h K_hᵀ / sqrt(d_head), S[i,j] = -inf for j > i, P = softmax_rows(S),
@@ -726,11 +726,12 @@ bool dh_supported(uint32_t d) { return d >= 8 && d <= 64 && d % 8 == 0; }
 
 int check_common(aur_ctx* ctx, uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head,
                  uint32_t ld_qkv, uint32_t ld_o) {
-  if (!dh_supported(d_head))
-    return aur::set_error(ctx, AUR_ELIMIT, "attention: d_head=%u, kernels support multiples of 8 up to 64",
-                          d_head);
+  if (d_head < 1 || d_head > 64)
+    return aur::set_error(ctx, AUR_ELIMIT, "attention: d_head=%u, supported 1..64 (the reference's "
+                          "one-thread-per-column backward, src/gpu/attention.rs:266-331)", d_head);
   if (b == 0 || t == 0 || n_head == 0) return aur::set_error(ctx, AUR_EINVAL, "attention: empty shape");
-  if (ld_qkv < n_head * d_head || ld_o < n_head * d_head || (ld_qkv & 3) || (ld_o & 3))
+  if (ld_qkv < n_head * d_head || ld_o < n_head * d_head ||
+      (dh_supported(d_head) && ((ld_qkv & 3) || (ld_o & 3))))
     return aur::set_error(ctx, AUR_EINVAL, "attention: bad row stride (%u, %u)", ld_qkv, ld_o);
   if (n_head > 65535 || b > 65535 || (t + TQ - 1) / TQ > 65535)
     return aur::set_error(ctx, AUR_ELIMIT, "attention: grid too large");
@@ -837,6 +838,40 @@ __global__ void __launch_bounds__(256, 5) mha_bwd_dq_direct_kernel(AttnArgs a) {
   }
 }
 
+// d_head that is not a multiple of 8 (any 1..64, as the reference's
+// kernels take): the heads are copied into a layout whose heads are padded
+// with zero columns to the next multiple of 8 — zero columns add nothing to
+// a score, an output row or a gradient — the kernels run at that width with
+// the true scale 1/sqrt(d_head), and the results are copied back.
+__global__ void __launch_bounds__(256) pad_heads_kernel(const float* __restrict__ src, int ld, int H, int dh,
+                                                        int dhp, float* __restrict__ dst, size_t rows) {
+  const size_t n = rows * H * dhp;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % dhp);
+    const size_t rh = i / dhp;
+    const int h = (int)(rh % H);
+    const size_t r = rh / H;
+    dst[i] = c < dh ? src[r * ld + (size_t)h * dh + c] : 0.f;
+  }
+}
+
+__global__ void __launch_bounds__(256) unpad_heads_kernel(const float* __restrict__ src, int H, int dh, int dhp,
+                                                          float* __restrict__ dst, int ld, size_t rows,
+                                                          int accumulate) {
+  const size_t n = rows * H * dh;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % dh);
+    const size_t rh = i / dh;
+    const int h = (int)(rh % H);
+    const size_t r = rh / H;
+    const float v = src[(r * H + h) * dhp + c];
+    float* p = dst + r * ld + (size_t)h * dh + c;
+    *p = accumulate ? *p + v : v;
+  }
+}
+
+unsigned pad_grid(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 8192); }
+
 template <int DH>
 void launch_fwd(const AttnArgs& a, int b, hipStream_t st) {
   dim3 grid(a.H, b, (a.T + TQ - 1) / TQ);
@@ -876,16 +911,45 @@ void launch_bwd(const AttnArgs& a, int b, hipStream_t st) {
 // tiled layout needs more than that (short or ragged t) D and the tiles go
 // to the context's workspace instead (refused while the stream is being
 // captured, since that workspace may be reallocated).
+// scale_dh: the d_head of the scale 1/sqrt(scale_dh) (the caller's, when the
+// heads arrive padded); 0 = d_head.
 static int mha_bwd_impl(aur_ctx* ctx, int overwrite, bool ws_tiled, const float* q, const float* k,
                         const float* v, uint32_t ld_qkv, const float* out, const float* d_out, uint32_t ld_out,
                         const float* lse, float* dq, float* dk, float* dv, uint32_t ld_dqkv, float* ws,
-                        uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head) {
+                        uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head, uint32_t scale_dh = 0) {
   AUR_CHECK_CTX(ctx);
   if (int rc = check_common(ctx, b, t, n_head, d_head, ld_qkv, ld_out)) return rc;
-  if (ld_dqkv < n_head * d_head || (ld_dqkv & 3))
+  if (ld_dqkv < n_head * d_head || (dh_supported(d_head) && (ld_dqkv & 3)))
     return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: bad gradient row stride %u", ld_dqkv);
   if (!q || !k || !v || !out || !d_out || !lse || !dq || !dk || !dv || !ws)
     return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: null pointer");
+  if (!dh_supported(d_head)) {
+    // padded heads (see pad_heads_kernel): q, k, v, o, dO and the three
+    // gradients at width dhp, then the tiled workspace, in the context's
+    // workspace; the kernels store the padded gradients, which are then
+    // added to (or stored into) the caller's
+    const uint32_t dhp = (d_head + 7) / 8 * 8;
+    const size_t rows = (size_t)b * t, n = rows * n_head * dhp;
+    if (int rc = aur::ensure_workspace(ctx, (8 * n + tiled_ws_floats(b, t, n_head)) * sizeof(float))) return rc;
+    float* P = static_cast<float*>(ctx->ws);
+    const float* srcs[5] = {q, k, v, out, d_out};
+    const uint32_t lds[5] = {ld_qkv, ld_qkv, ld_qkv, ld_out, ld_out};
+    for (int i = 0; i < 5; ++i)
+      hipLaunchKernelGGL(pad_heads_kernel, dim3(pad_grid(n)), dim3(256), 0, ctx->stream, srcs[i], (int)lds[i],
+                         (int)n_head, (int)d_head, (int)dhp, P + i * n, rows);
+    AUR_LAUNCH_CHECK(ctx, "pad_heads_kernel");
+    const uint32_t ldp = n_head * dhp;
+    if (int rc = mha_bwd_impl(ctx, 1, true, P, P + n, P + 2 * n, ldp, P + 3 * n, P + 4 * n, ldp, lse, P + 5 * n,
+                              P + 6 * n, P + 7 * n, ldp, P + 8 * n, b, t, n_head, dhp, d_head))
+      return rc;
+    float* dsts[3] = {dq, dk, dv};
+    for (int i = 0; i < 3; ++i)
+      hipLaunchKernelGGL(unpad_heads_kernel, dim3(pad_grid(rows * n_head * d_head)), dim3(256), 0, ctx->stream,
+                         P + (5 + i) * n, (int)n_head, (int)d_head, (int)dhp, dsts[i], (int)ld_dqkv, rows,
+                         overwrite ? 0 : 1);
+    AUR_LAUNCH_CHECK(ctx, "unpad_heads_kernel");
+    return 0;
+  }
   if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(d_out) || !al16(dq) || !al16(dk) ||
       !al16(dv) || !al16(ws))
     return aur::set_error(ctx, AUR_EINVAL, "mha_bwd: tensors must be 16-byte aligned");
@@ -902,7 +966,7 @@ static int mha_bwd_impl(aur_ctx* ctx, int overwrite, bool ws_tiled, const float*
   a.ntri = (int)(((t + TQ - 1) / TQ) * ((t + TQ - 1) / TQ + 1) / 2);
   a.ld_qkv = (int)ld_qkv; a.ld_o = (int)ld_out; a.ld_d = (int)ld_dqkv;
   a.T = (int)t; a.H = (int)n_head;
-  a.scale = 1.0f / sqrtf((float)d_head);
+  a.scale = 1.0f / sqrtf((float)(scale_dh ? scale_dh : d_head));
   switch (d_head) {
     case 8: launch_bwd<8>(a, (int)b, ctx->stream); break;
     case 16: launch_bwd<16>(a, (int)b, ctx->stream); break;
@@ -926,13 +990,34 @@ int aur_mha_fwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v,
   AUR_CHECK_CTX(ctx);
   if (int rc = check_common(ctx, b, t, n_head, d_head, ld_qkv, ld_out)) return rc;
   if (!q || !k || !v || !out || !lse) return aur::set_error(ctx, AUR_EINVAL, "mha_fwd: null pointer");
-  if (!al16(q) || !al16(k) || !al16(v) || !al16(out))
+  uint32_t scale_dh = d_head;
+  float* out_p = nullptr;  // padded output to copy back
+  const size_t rows = (size_t)b * t;
+  const uint32_t d_user = d_head, ld_out_user = ld_out;
+  float* out_user = out;
+  if (!dh_supported(d_head)) {
+    // padded heads (see pad_heads_kernel): q, k, v and the output at width
+    // dhp in the context's workspace
+    const uint32_t dhp = (d_head + 7) / 8 * 8;
+    const size_t n = rows * n_head * dhp;
+    if (int rc = aur::ensure_workspace(ctx, 4 * n * sizeof(float))) return rc;
+    float* P = static_cast<float*>(ctx->ws);
+    const float* srcs[3] = {q, k, v};
+    for (int i = 0; i < 3; ++i)
+      hipLaunchKernelGGL(pad_heads_kernel, dim3(pad_grid(n)), dim3(256), 0, ctx->stream, srcs[i], (int)ld_qkv,
+                         (int)n_head, (int)d_head, (int)dhp, P + i * n, rows);
+    AUR_LAUNCH_CHECK(ctx, "pad_heads_kernel");
+    q = P; k = P + n; v = P + 2 * n; out = out_p = P + 3 * n;
+    ld_qkv = ld_out = n_head * dhp;
+    d_head = dhp;
+  } else if (!al16(q) || !al16(k) || !al16(v) || !al16(out)) {
     return aur::set_error(ctx, AUR_EINVAL, "mha_fwd: tensors must be 16-byte aligned");
+  }
   AttnArgs a{};
   a.q = q; a.k = k; a.v = v; a.out = out; a.lse = lse;
   a.ld_qkv = (int)ld_qkv; a.ld_o = (int)ld_out;
   a.T = (int)t; a.H = (int)n_head;
-  a.scale = 1.0f / sqrtf((float)d_head);
+  a.scale = 1.0f / sqrtf((float)scale_dh);
   switch (d_head) {
     case 8: launch_fwd<8>(a, (int)b, ctx->stream); break;
     case 16: launch_fwd<16>(a, (int)b, ctx->stream); break;
@@ -944,6 +1029,11 @@ int aur_mha_fwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v,
     default: launch_fwd<64>(a, (int)b, ctx->stream); break;
   }
   AUR_LAUNCH_CHECK(ctx, "mha_fwd_kernel");
+  if (out_p) {
+    hipLaunchKernelGGL(unpad_heads_kernel, dim3(pad_grid(rows * n_head * d_user)), dim3(256), 0, ctx->stream,
+                       out_p, (int)n_head, (int)d_user, (int)d_head, out_user, (int)ld_out_user, rows, 0);
+    AUR_LAUNCH_CHECK(ctx, "unpad_heads_kernel");
+  }
   return 0;
 }
 

@@ -420,6 +420,59 @@ __global__ void __launch_bounds__(64 * SW) kv_seq_kernel(KvArgs a, int t_max) {
   }
 }
 
+// Any d_head (the reference's kernel stride-loops over the head's columns,
+// src/gpu/kv_cache.rs:339-348): one block per (head, sequence); a thread per
+// key computes its score (scalar loads: d_head need not allow float4), the
+// scores live in LDS (dynamic, t_max floats), the block takes their max and
+// sum, and a thread per output column sums p_j·v_j over the keys.  A
+// generality path, not a bandwidth-shaped one; no fused append, no
+// partials.
+__device__ float block_reduce(float v, float* red, bool is_max) {
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float o = __shfl_xor(v, m, 64);
+    v = is_max ? fmaxf(v, o) : v + o;
+  }
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();  // red is reused
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < nw; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+  return r;
+}
+
+__global__ void __launch_bounds__(256) kv_generic_kernel(KvArgs a, int t_max, int dh) {
+  extern __shared__ float sc[];
+  __shared__ float red[4];
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int T = min(a.t_dev ? a.t_dev[b] : a.t_scalar, t_max);
+  const float* q = a.q + (size_t)b * a.ld_q + (size_t)h * dh;
+  const size_t hist = (size_t)b * a.max_len, col = (size_t)h * dh;
+  float mx = -INFINITY;
+  for (int j = threadIdx.x; j < T; j += blockDim.x) {
+    const float* k = a.kh + (hist + j) * a.ld + col;
+    float s = 0.f;
+    for (int c = 0; c < dh; ++c) s += q[c] * k[c];
+    s *= a.scale;
+    sc[j] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = block_reduce(mx, red, true);
+  float sum = 0.f;
+  for (int j = threadIdx.x; j < T; j += blockDim.x) {
+    const float e = expf(sc[j] - mx);
+    sc[j] = e;
+    sum += e;
+  }
+  sum = block_reduce(sum, red, false);  // its barriers also publish sc
+  const float inv = sum > 0.f ? 1.f / sum : 0.f;
+  for (int c = threadIdx.x; c < dh; c += blockDim.x) {
+    float acc = 0.f;
+    for (int j = 0; j < T; ++j) acc += sc[j] * inv * a.vh[(hist + j) * a.ld + col + c];
+    a.out[(size_t)b * a.ld + col + c] = acc;
+  }
+}
+
 template <int DH>
 __global__ void __launch_bounds__(64) kv_combine_kernel(KvArgs a) {
   merge_chunks<DH>(a, blockIdx.y, blockIdx.x, threadIdx.x);
@@ -459,7 +512,21 @@ void launch_seq(const KvArgs& a, int B, int t_max, hipStream_t st) {
 // of KC) the scratch-free one-block-per-(sequence, head) kernel runs.
 bool chunks_fit(int max_len) { return (long)((max_len + KC - 1) / KC) * PART <= max_len; }
 
+// d_head of the bandwidth-shaped kernels; any other takes kv_generic_kernel.
+bool dh_ok(uint32_t d) { return d >= 8 && d <= 64 && d % 8 == 0; }
+
+constexpr int kGenericMaxKeys = 16384;  // LDS scores of kv_generic_kernel (64 KiB)
+
 int launch(aur_ctx* ctx, KvArgs& a, int B, int t_max, int d_head) {
+  if (!dh_ok((uint32_t)d_head)) {
+    if (t_max > kGenericMaxKeys)
+      return aur::set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%d takes the generic kernel, which holds at "
+                            "most %d keys", d_head, kGenericMaxKeys);
+    hipLaunchKernelGGL(kv_generic_kernel, dim3(a.H, B), dim3(256), (size_t)t_max * sizeof(float), ctx->stream, a,
+                       t_max, d_head);
+    AUR_LAUNCH_CHECK(ctx, "kv_generic_kernel");
+    return 0;
+  }
   a.nch = (t_max + KC - 1) / KC;
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   const bool seq = ((long)B * a.H >= cus && std::getenv("AUR_KV_CHUNKED") == nullptr) ||
@@ -481,8 +548,6 @@ int launch(aur_ctx* ctx, KvArgs& a, int B, int t_max, int d_head) {
   return 0;
 }
 
-bool dh_ok(uint32_t d) { return d >= 8 && d <= 64 && d % 8 == 0; }
-
 bool aligned16_kv(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -498,8 +563,7 @@ int aur_mha_kv_step(aur_ctx* ctx, const float* q_new, const float* k_history, co
                     float* out, float* scratch, uint32_t t_total, uint32_t n_head, uint32_t d_head,
                     uint32_t max_len) {
   AUR_CHECK_CTX(ctx);
-  if (!dh_ok(d_head))
-    return aur::set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%u, supports multiples of 8 up to 64", d_head);
+  if (d_head == 0) return aur::set_error(ctx, AUR_EINVAL, "mha_kv_step: d_head=0");
   if (t_total == 0 || t_total > max_len || n_head == 0)
     return aur::set_error(ctx, AUR_EINVAL, "mha_kv_step: t_total=%u max_len=%u", t_total, max_len);
   if (!q_new || !k_history || !v_history || !out || !scratch)
@@ -530,9 +594,12 @@ int mha_kv_batched(aur_ctx* ctx, const float* q, int ld_q, const float* k_histor
                    const float* v_history, float* out, float* scratch, const int32_t* t_total, int t_max,
                    int b, int n_head, int d_head, int max_len, const float* k_new, const float* v_new,
                    int nparts, size_t part_stride, const L2Prefetch* prefetch) {
-  if (!dh_ok((uint32_t)d_head))
-    return set_error(ctx, AUR_ELIMIT, "mha_kv_step: d_head=%d, supports multiples of 8 up to 64", d_head);
-  if (b <= 0 || n_head <= 0 || t_max <= 0 || t_max > max_len || ld_q < n_head * d_head || (ld_q & 3))
+  if (d_head <= 0) return set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: d_head=%d", d_head);
+  if (!dh_ok((uint32_t)d_head) && (k_new || v_new || nparts > 1))
+    return set_error(ctx, AUR_ELIMIT, "mha_kv_step_batched: the fused append and QKV partials need d_head a "
+                     "multiple of 8 up to 64 (d_head=%d)", d_head);
+  if (b <= 0 || n_head <= 0 || t_max <= 0 || t_max > max_len || ld_q < n_head * d_head ||
+      (dh_ok((uint32_t)d_head) && (ld_q & 3)))
     return set_error(ctx, AUR_EINVAL, "mha_kv_step_batched: b=%d t_max=%d max_len=%d ld_q=%d", b, t_max,
                      max_len, ld_q);
   if (!q || !k_history || !v_history || !out || !scratch || !t_total || (!k_new != !v_new))

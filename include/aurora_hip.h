@@ -137,8 +137,12 @@ int aur_gemm_ex(aur_ctx* ctx, int a_kcontig, int b_kcontig,
  * reads back (it is only the forward→backward hand-off).
  * Replaces CausalMhaForwardKernel::dispatch_into(ctx, enc, q, k, v, out,
  * probs, t, n_head, d_head) (src/gpu/attention.rs:400-443).
- * Limits: d_head a multiple of 8 up to 64 (AUR_ELIMIT otherwise); any t >= 1;
- * q/k/v/out 16-byte aligned. */
+ * Limits: any d_head from 1 to 64 (AUR_ELIMIT above, as the reference's
+ * one-thread-per-column backward, src/gpu/attention.rs:266-331); multiples
+ * of 8 run in place and need q/k/v/out 16-byte aligned, any other d_head
+ * runs on zero-padded copies of the heads in the context's workspace
+ * (allocated on first need, so not while the stream is being captured);
+ * any t >= 1. */
 int aur_mha_fwd(aur_ctx* ctx, const float* q, const float* k, const float* v,
                 float* out, float* lse,
                 uint32_t b, uint32_t t, uint32_t n_head, uint32_t d_head);
@@ -182,7 +186,11 @@ int aur_mha_bwd_ex(aur_ctx* ctx, const float* q, const float* k, const float* v,
  * aur_mha_kv_ws_bytes(1, n_head, max_len) bytes, which never exceeds the
  * reference's n_head·max_len floats (src/gpu/transformer.rs:2432): 68-float
  * records per 128 keys where a full history's records fit in that, else 0
- * bytes (the scratch-free one-block-per-head kernel runs).
+ * bytes (the scratch-free one-block-per-head kernel runs).  Any d_head >= 1
+ * (the reference stride-loops over the head's columns, src/gpu/kv_cache.rs:
+ * 339-348): multiples of 8 up to 64 take the bandwidth-shaped kernels, any
+ * other d_head a generic one that keeps the scores of up to 16384 keys in
+ * LDS (AUR_ELIMIT beyond).
  * Replaces MhaKvCacheKernel::dispatch_into(ctx, enc, q_new, k_history,
  * v_history, out, scratch, t_total, n_head, d_head, max_len)
  * (src/gpu/kv_cache.rs:421-465). */

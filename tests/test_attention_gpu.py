@@ -390,3 +390,50 @@ def test_kv_step_within_reference_scratch_allocation(ctx, max_len, t_total, H, d
     assert _guards_intact(guard, n_s)
     want = oracle.kv_attend(q_new, kh, vh, t_total, H, dh)
     assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
+
+
+# ------------------------------------------------ any d_head (the reference's)
+@pytest.mark.parametrize("B,t,H,dh", [(1, 6, 2, 1), (2, 37, 3, 12), (1, 70, 2, 20), (2, 65, 1, 36), (1, 9, 4, 60),
+                                      (1, 130, 2, 63)])
+def test_forward_backward_any_d_head(ctx, B, t, H, dh):
+    """The reference's training kernels take any d_head ≤ 64 (one thread per
+    column with a guard, src/gpu/attention.rs:266-331); here d_head that is
+    not a multiple of 8 runs through zero-padded heads.  Forward, LSE and
+    the accumulated gradients (onto non-zero destinations) against float64."""
+    rng = np.random.default_rng(B * 1000 + t * 10 + dh)
+    n = B * t * H * dh
+    q, k, v, do = (_n(rng, n) for _ in range(4))
+    out, lse = _fwd(ctx, q, k, v, B, t, H, dh)
+    shp = (B, t, H, dh)
+    o64, l64 = causal_attention_f64(*(x.reshape(shp).astype(np.float64) for x in (q, k, v)))
+    assert fro_rel(out, o64) < TOL_ATTN and max_norm_rel(out, o64) < TOL_ATTN
+    np.testing.assert_allclose(lse.reshape(B, H, t), l64, rtol=0, atol=1e-4)
+    init = [_n(rng, n) for _ in range(3)]
+    grads = _bwd(ctx, q, k, v, out, lse, do, B, t, H, dh, init=init)
+    g64 = causal_attention_grad_f64(*(x.reshape(shp).astype(np.float64) for x in (q, k, v, do)))
+    for got, want, base in zip(grads, g64, init):
+        d = got.astype(np.float64) - base
+        assert fro_rel(d, want) < TOL_ATTN and max_norm_rel(d, want) < TOL_ATTN
+
+
+def test_any_d_head_beyond_64_refused(ctx):
+    from aurora_amd._lib import AuroraError
+
+    with pytest.raises(AuroraError) as e:
+        _fwd(ctx, *(np.zeros(4 * 2 * 72, np.float32) for _ in range(3)), 1, 4, 2, 72)
+    assert e.value.code == 10003
+
+
+@pytest.mark.parametrize("t_total,H,dh,max_len", [(5, 2, 12, 8), (80, 3, 20, 96), (129, 2, 100, 130),
+                                                  (300, 1, 128, 300), (64, 4, 6, 64), (33, 2, 1, 40)])
+def test_kv_step_any_d_head(ctx, t_total, H, dh, max_len):
+    """src/gpu/kv_cache.rs:339-348 stride-loops over d_head, past 64 too:
+    d_head that the bandwidth-shaped kernels do not take runs the generic
+    kernel; against the oracle."""
+    d = H * dh
+    rng = np.random.default_rng(t_total * 7 + dh)
+    q_new = _n(rng, d)
+    kh, vh = _n(rng, max_len * d), _n(rng, max_len * d)
+    got = _kv_single(ctx, q_new, kh, vh, t_total, H, dh, max_len)
+    want = oracle.kv_attend(q_new, kh, vh, t_total, H, dh)
+    assert fro_rel(got, want) < TOL_ATTN and max_norm_rel(got, want) < TOL_ATTN
