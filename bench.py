@@ -397,6 +397,28 @@ def bench_vendor(steps: int) -> None:
             res[form] = 2.0 * m * n * k / (e0.elapsed_time(e1) / steps * 1e-3) / 1e12
         log(f"[bench] vendor {m}x{n}x{k}: NT {res['NT']:.1f} NN {res['NN']:.1f} TFLOP/s")
         del x, w, wt
+    # the weight-gradient accumulate dest[d_out, d_in] += dYᵀ·X (both operands
+    # k-strided: t runs down their rows) as torch.addmm on transposed views
+    for d_out, d_in, t in ((2048, 512, 8192), (3072, 1024, 16384), (1024, 1024, 16384), (4096, 1024, 16384),
+                           (1024, 4096, 16384), (8192, 1024, 16384)):
+        dy = torch.rand(t, d_out, device=dev) - 0.5
+        x = torch.rand(t, d_in, device=dev) - 0.5
+        dest = torch.rand(d_out, d_in, device=dev) - 0.5
+        fn = lambda: dest.addmm_(dy.t(), x)  # noqa: E731
+        end = time.perf_counter() + CLOCK_RAMP_S
+        while time.perf_counter() < end:
+            for _ in range(10):
+                fn()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        tf = 2.0 * d_out * d_in * t / (e0.elapsed_time(e1) / steps * 1e-3) / 1e12
+        log(f"[bench] vendor acc {d_out}x{d_in}_t{t}: {tf:.1f} TFLOP/s")
+        del dy, x, dest
 
 
 C3 = dict(vocab=8192, d_model=1024, n_layer=12, n_head=16, d_ff=4096, seq_len_max=1024)
