@@ -45,7 +45,7 @@ struct AttnArgs {
   float* out;        // forward output
   float* lse;        // [B, H, T]
   float* D;          // [B, H, T] rowdot
-  float* ds;         // [B, H, ntri, 64, 64] dS tiles of the causal lower triangle
+  float* ds;         // [B, H, ntri] 64×64 dS tiles of the causal lower triangle (ds_slot)
   int ntri;          // nqt·(nqt+1)/2 tiles per (sequence, head)
   float* dq;
   float* dk;
@@ -443,6 +443,18 @@ __global__ void __launch_bounds__(256, 4) mha_fwd_direct_kernel(AttnArgs a) {
   }
 }
 
+// Layout of one 64×64 dS tile in the workspace: four 16-key blocks of 1024
+// floats (key block kb = key / 16 at kb·1024), each holding 64 query slots of
+// 16 keys (64 bytes).  Query q of sub-tile q / 16 sits in slot 16·(q / 16) +
+// slot_of(q % 16), slot_of(4g + e) = 2e + 8·(g / 2) + g % 2: the four rows
+// 4g + e (g = 0..3) a wave's accumulator register e holds go to slots 2e,
+// 2e + 1, 2e + 8, 2e + 9, so each store instruction of pass 2 writes two
+// whole 128-byte lines, and a pass-3 wave's 16 query rows of one key block
+// are one contiguous KB.
+__device__ __forceinline__ int ds_slot(int r16) {  // r16 = q % 16
+  return 2 * (r16 & 3) + 8 * (r16 >> 3) + ((r16 >> 2) & 1);
+}
+
 // ------------------------------------------------- backward pass 1: rowdot
 // D[b,h,i] = Σ_c dO[i,c]·O[i,c]  (= Σ_j P_ij dP_ij of the reference's fused
 // dscores pass, src/gpu/attention.rs:163-247).  One lane per float4 of the
@@ -585,13 +597,13 @@ __global__ void __launch_bounds__(256, (NS == 1 ? 3 : 1)) mha_bwd_dkv_kernel(Att
         if (qt == kt && krow > q) pe = 0.f;
         p[e] = pe;
         ds[e] = pe * (dp[e] - Dq[e]);
-        // dS tile (qt, kt), row-major [q][key], for the dQ pass.  Streamed
+        // dS tile (qt, kt) for the dQ pass, in the ds_slot layout (this
+        // wave's key block; row 4g + e in slot ds_slot(4g + e)).  Streamed
         // (non-temporal): it is read back only after the whole pass, and
         // keeping it out of L2 leaves room for the Q / dO tiles this block
-        // and its neighbours re-read (at B16 H8 T1024 this pass fetches
-        // 280-380 MB instead of 432 MB, and writes 432 MB instead of 345:
-        // the two waves' halves of a line are no longer merged in L2).
-        __builtin_nontemporal_store(ds[e], &ds_tile[(16 * jq + 4 * g + e) * TQ + 16 * w + l16]);
+        // and its neighbours re-read.
+        __builtin_nontemporal_store(
+            ds[e], &ds_tile[w * (16 * TQ) + (16 * jq + 2 * e + 8 * (g >> 1) + (g & 1)) * 16 + l16]);
       }
       // dVᵀ[d][key] += dOᵀ[d][q]·P[q][key];  dKᵀ[d][key] += Qᵀ[d][q]·dS[q][key]
 #pragma unroll
@@ -634,7 +646,7 @@ __global__ void __launch_bounds__(256, (NS == 1 ? 3 : 1)) mha_bwd_dkv_kernel(Att
 // dQ[q] = scale · Σ_key dS[q][key] K[key] over the key tiles 0..qt of this
 // query tile, in increasing key order, from the dS tiles pass 2 stored.  A
 // wave owns 16 query rows; lane l reads dS[16w + l%16][16j + 4·(l/16) .. +3]
-// (one float4 per 16-key sub-tile j), which is exactly the B operand of
+// (one float4 per 16-key block j, from the row's ds_slot), which is exactly the B operand of
 // dQᵀ[d][q] += Kᵀ[d][key]·dSᵀ[key][q] in the Sᵀ layout of the other passes.
 // K tiles go through LDS double-buffered, the next tile's dS fragments are
 // loaded into registers while the current ones are multiplied.  On the
@@ -652,13 +664,14 @@ __global__ void __launch_bounds__(256) mha_bwd_dq_kernel(AttnArgs a) {
   const int h = blockIdx.x, b = blockIdx.y;
   const size_t row_base = (size_t)b * a.T;
   const float* Kb = a.k + row_base * a.ld_qkv + h * DH;
-  // dS tile (qt, kt) at tiles + kt·TQ², this lane's row and column offset folded in
+  // dS tile (qt, kt) at tiles + kt·TQ², this lane's row slot and keys folded in
   const float* tiles = a.ds + (((size_t)b * a.H + h) * a.ntri + qt * (qt + 1) / 2) * (TQ * TQ) +
-                       (16 * w + l16) * TQ + 4 * g;
+                       (16 * w + ds_slot(l16)) * 16 + 4 * g;
   auto load_ds = [&](int kt, floatx4* f) {  // read once: streamed past L2
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      f[j] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + 16 * j));
+      f[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + j * (16 * TQ)));
   };
 
   floatx4 acc[NC];
@@ -755,12 +768,13 @@ __global__ void __launch_bounds__(256, 5) mha_bwd_dq_direct_kernel(AttnArgs a) {
   const size_t row_base = (size_t)b * a.T;
   const float* Kb = a.k + row_base * a.ld_qkv + h * DH;
   const float* tiles = a.ds + (((size_t)b * a.H + h) * a.ntri + qt * (qt + 1) / 2) * (TQ * TQ) +
-                       (16 * w + l16) * TQ + 4 * g;
+                       (16 * w + ds_slot(l16)) * 16 + 4 * g;
   auto load_ds = [&](int kt, floatx4* f) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // read once: streamed past L2, which keeps the K tiles
-      f[j] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + 16 * j));
+      f[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const floatx4*>(tiles + (size_t)kt * (TQ * TQ) + j * (16 * TQ)));
     }
   };
   auto issue_k = [&](int kt, float* lds) {
