@@ -123,9 +123,12 @@ void DecoderTransformerGpu::init() {
   if (!ctx || V == 0 || d == 0 || L == 0 || F == 0 || Tm == 0 || max_batch == 0 || cfg.n_head == 0 ||
       d % cfg.n_head != 0)
     throw Error("DecoderTransformerGpu: invalid config", AUR_EINVAL);
+  // d_head up to 64, as the reference's one-thread-per-column attention
+  // backward takes (src/gpu/attention.rs:266-331); multiples of 8 run the
+  // attention kernels in place, any other d_head on zero-padded head copies
+  // (training) and the generic KV kernel (decode).
   const uint32_t dh = cfg.d_model / cfg.n_head;
-  if (dh % 8 != 0 || dh > 64)
-    throw Error("DecoderTransformerGpu: d_head must be a multiple of 8 up to 64", AUR_ELIMIT);
+  if (dh > 64) throw Error("DecoderTransformerGpu: d_head must be at most 64", AUR_ELIMIT);
   if (d % 4 != 0 || F % 4 != 0 || V % 4 != 0)
     throw Error("DecoderTransformerGpu: vocab, d_model, d_ff must be multiples of 4", AUR_EINVAL);
   // Flat parameter layout: weight-decayed tensors first (w_tok, then per
@@ -723,7 +726,8 @@ KvCacheGpu::KvCacheGpu(DecoderTransformerGpu& model, uint32_t batch_, uint32_t m
     // The decode QKV projection as qkv_parts K-range partials [parts][B][3d]
     // that the attention kernel sums; W_o / W_proj as K-range partials
     // [splits][B][d] that the following LayerNorm sums.
-    qkv_parts = split_override(0, qkv_splits(d), d, 8);
+    // (the attention kernel that sums them takes d_head a multiple of 8)
+    if ((d / c.n_head) % 8 == 0) qkv_parts = split_override(0, qkv_splits(d), d, 8);
     o_parts = split_override(1, aur::gemm_nt_partials_splits((int)B, (int)d, (int)d), d, 64);
     p_parts = split_override(2, aur::gemm_nt_partials_splits((int)B, (int)d, (int)F), F, 64);
   }
@@ -935,10 +939,22 @@ void DecoderTransformerGpu::encode_decode_step(KvCacheGpu& cache) {
         if (*c == 'p') add(Y.w_proj, d, F, split ? 64 : 16);
       }
     }
-    ck(ctx_, aur::mha_kv_batched(ctx_, cache.qkv_, 3 * d, cache.k_history(l), cache.v_history(l), cache.attn_,
-                                 cache.scratch_, cache.lens_, t_max, B, H, dh, (int)cache.max_len,
-                                 cache.qkv_ + d, cache.qkv_ + 2 * d, cache.qkv_parts, (size_t)B * 3 * d, &pf),
-       "mha_kv");
+    if (dh % 8 == 0) {
+      ck(ctx_, aur::mha_kv_batched(ctx_, cache.qkv_, 3 * d, cache.k_history(l), cache.v_history(l), cache.attn_,
+                                   cache.scratch_, cache.lens_, t_max, B, H, dh, (int)cache.max_len,
+                                   cache.qkv_ + d, cache.qkv_ + 2 * d, cache.qkv_parts, (size_t)B * 3 * d, &pf),
+         "mha_kv");
+    } else {
+      // other d_head: the new K/V rows appended at each sequence's position
+      // first, then the generic KV kernel over the history
+      ck(ctx_, aur::kv_store(ctx_, cache.qkv_, d, cache.k_history(l), cache.v_history(l), (int)cache.max_len,
+                             cache.pos_, B, 1),
+         "kv_store");
+      ck(ctx_, aur::mha_kv_batched(ctx_, cache.qkv_, 3 * d, cache.k_history(l), cache.v_history(l), cache.attn_,
+                                   cache.scratch_, cache.lens_, t_max, B, H, dh, (int)cache.max_len, nullptr,
+                                   nullptr, 1, 0, nullptr),
+         "mha_kv");
+    }
     if (split) {
       ck(ctx_, aur::gemm_nt_partials(ctx_, cache.attn_, d, Y.w_o, d, cache.part_, B, d, d, s_o), "w_o");
       ck(ctx_, aur::layer_norm_forward_sum(ctx_, cache.x_, cache.part_, s_o, cache.xmid_, Y.ln2_g, Y.ln2_b,

@@ -225,7 +225,11 @@ typedef struct {
 /* DecoderTransformerGpu::from_cpu (transformer.rs:949) without the upload:
  * allocates parameters (zero), gradients, AdamW moments and the activation
  * arena for max_batch × seq_len_max rows.  Parameters are then written
- * through aur_model_tensor pointers. */
+ * through aur_model_tensor pointers.  Limits: d_model a multiple of n_head
+ * with d_head = d_model / n_head up to 64 (AUR_ELIMIT above; d_head not a
+ * multiple of 8 trains on zero-padded head copies in the context's workspace
+ * and decodes through the generic KV kernel); vocab, d_model and d_ff
+ * multiples of 4. */
 int aur_model_create(aur_ctx* ctx, const aur_model_config* cfg, uint32_t max_batch, aur_model** out);
 int aur_model_destroy(aur_model* m);
 /* Device pointer + length of a parameter (grad = 0) or its gradient

@@ -117,11 +117,12 @@ def test_train_step_wide_rows_matches_cpu(ctx, d, B, T):
     m.destroy()
 
 
-@pytest.mark.parametrize("dh", [24, 40, 48, 56])
+@pytest.mark.parametrize("dh", [24, 40, 48, 56, 12, 20, 5])
 def test_train_step_head_widths_match_cpu(ctx, dh):
-    """d_head values that are multiples of 8 but not of 16 (the reference
-    takes any d_head ≤ 64): one train step over 2 × 70 rows against the
-    oracle, every gradient."""
+    """d_head values that are multiples of 8 but not of 16, and ones that
+    are not multiples of 8 (zero-padded heads), as the reference takes any
+    d_head ≤ 64: one train step over 2 × 70 rows against the oracle, every
+    gradient."""
     H = 4
     cfg = OM.Config(vocab=128, d_model=H * dh, n_layer=1, n_head=H, d_ff=2 * H * dh, seq_len_max=80)
     P = OM.init_params(cfg, 7)
@@ -407,13 +408,15 @@ def test_kv_decode_above_64_sequences_matches_cpu(ctx):
 
 
 @pytest.mark.parametrize("d,H,F", [(384, 6, 1536), (768, 12, 3072), (640, 10, 2560), (384, 8, 1536),
-                                   (96, 4, 192)])
+                                   (96, 4, 192), (48, 4, 96), (80, 4, 160)])
 def test_kv_decode_widths_match_cpu(ctx, d, H, F):
     """Decode at the reference's TransformerConfig::nano width (d 384, H 6,
     d_ff 1536; src/transformer/model.rs:87-96) and at d 768 / 640: K = 384,
     768, 1536, 2560, 3072 give split counts whose K ranges must all be
     non-empty (the W_o / W_proj partial products); d 384 with 8 heads and
-    d 96 with 4 give d_head 48 and 24."""
+    d 96 with 4 give d_head 48 and 24; d 48 and 80 with 4 heads give d_head
+    12 and 20 (the new K/V rows appended by their own launch, the generic KV
+    kernel, prefill through the padded attention)."""
     cfg = OM.Config(vocab=96, d_model=d, n_layer=2, n_head=H, d_ff=F, seq_len_max=48)
     P = OM.init_params(cfg, 17)
     B, T0, steps = 2, 20, 4
