@@ -416,6 +416,18 @@ def test_forward_backward_any_d_head(ctx, B, t, H, dh):
         assert fro_rel(d, want) < TOL_ATTN and max_norm_rel(d, want) < TOL_ATTN
 
 
+def test_kv_step_generic_beyond_16384_keys_refused(ctx):
+    """The generic KV kernel keeps a sequence's scores in LDS: a history past
+    16384 keys with a d_head it serves is refused (AUR_ELIMIT) before launch."""
+    from aurora_amd._lib import AuroraError
+
+    H, dh, t = 1, 12, 16385
+    z = np.zeros(t * H * dh, np.float32)
+    with pytest.raises(AuroraError) as e:
+        _kv_single(ctx, np.zeros(H * dh, np.float32), z, z, t, H, dh, t)
+    assert e.value.code == 10003
+
+
 def test_any_d_head_beyond_64_refused(ctx):
     from aurora_amd._lib import AuroraError
 
@@ -425,11 +437,13 @@ def test_any_d_head_beyond_64_refused(ctx):
 
 
 @pytest.mark.parametrize("t_total,H,dh,max_len", [(5, 2, 12, 8), (80, 3, 20, 96), (129, 2, 100, 130),
-                                                  (300, 1, 128, 300), (64, 4, 6, 64), (33, 2, 1, 40)])
+                                                  (300, 1, 128, 300), (64, 4, 6, 64), (33, 2, 1, 40),
+                                                  (16384, 1, 12, 16384)])
 def test_kv_step_any_d_head(ctx, t_total, H, dh, max_len):
     """src/gpu/kv_cache.rs:339-348 stride-loops over d_head, past 64 too:
     d_head that the bandwidth-shaped kernels do not take runs the generic
-    kernel; against the oracle."""
+    kernel (up to 16384 keys, its LDS score buffer, which the last case
+    fills); against the oracle."""
     d = H * dh
     rng = np.random.default_rng(t_total * 7 + dh)
     q_new = _n(rng, d)
